@@ -1,0 +1,95 @@
+/*
+ * tsa.h -- C-ABI of the MI355X (gfx950) attention + Gated DeltaNet kernels.
+ *
+ * Drop-in boundary for the two hot-path labs of cookys/turing-sm75.  Every entry point
+ * takes device pointers to contiguous buffers the caller owns, enqueues work on the
+ * given HIP stream (NULL = the default stream) and returns at once; nothing is
+ * allocated, nothing is synchronised, no process-global state is mutated.  Errors come
+ * back as TSA_* codes, never as exit() or exceptions (the reference's CUDA_CHECK exits,
+ * src/attn_sm75.cu:40-48).
+ *
+ * dtypes: q/k/v/o/out are IEEE fp16 (passed as void*), g_log, beta and the GDN state are
+ * fp32.  Layouts follow the reference:
+ *   attention : Q, K, V, O                [B][H][S][D]     (src/attn_sm75.cu:64,120,254)
+ *   GDN       : q, k                      [B][T][Hq][dk]   (src/gdn_sm75.cu:75-77)
+ *               v, out                    [B][T][Hv][dv]
+ *               g_log, beta               [B][T][Hv]
+ *               state                     [B][Hv][dv][dk]  (S[c*dk + i] = S[i][c], :71-72)
+ *   V-head h reads QK head h % Hq (src/gdn_sm75.cu:11,68).  The reference has B = 1.
+ */
+#ifndef TSA_H
+#define TSA_H
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TSA_OK = 0,
+    TSA_ERR_NULL = 1,        /* a required pointer is NULL                           */
+    TSA_ERR_SHAPE = 2,       /* a size is < 1, too large, or the shapes disagree      */
+    TSA_ERR_UNSUPPORTED = 3, /* a valid shape this build has no kernel for (e.g. D)  */
+    TSA_ERR_WORKSPACE = 4,   /* workspace NULL or smaller than *_workspace_bytes     */
+    TSA_ERR_LAUNCH = 5,      /* the HIP runtime rejected a launch                    */
+    TSA_ERR_ARG = 6          /* a non-shape argument is invalid (scale not finite...) */
+};
+
+/* Message for a TSA_* code (static storage). */
+const char* tsa_strerror(int code);
+/* Library version string, e.g. "tsa 0.1 gfx950". */
+const char* tsa_version(void);
+
+/* Softmax flash-attention forward, O = softmax(scale * Q K^T [+ causal mask]) V.
+ * Replaces launch_wmma<D> / launch_ffma<D> (src/attn_sm75.cu:421-440, dispatched on D at
+ * :481-488) and its kernel flash_attn_sm75_wmma (:239-375).  D in {64, 128}; any S >= 1
+ * (the reference caps S at 1024 for its naive check only, :457-460); causal 0 or 1 (the
+ * reference hard-codes 1, :463).  fp32 softmax statistics, fp16 MFMA. */
+int tsa_attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
+                 int D, float scale, int causal, void* stream);
+
+/* The lab's naive correctness kernel on the device: one thread per query row, fp32 dot
+ * products, two-pass exact softmax.  Same math as naive_attn_kernel
+ * (src/attn_sm75.cu:55-94) without its per-d recomputation of the dot product and without
+ * its S <= 1024 threads-per-block limit.  Used by the attn_sm75 driver's error check. */
+int tsa_attn_naive(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
+                   int D, float scale, int causal, void* stream);
+
+/* Chunked Gated DeltaNet prefill over T tokens for B sequences, state carried in place.
+ * Replaces the chunked kernels gdn_wmma_kernel (src/gdn_sm75.cu:361-574),
+ * gdn_chunked_kernel (:192-354) and the two-pass gdn_prep_kernel + gdn_apply_kernel
+ * (:896-1073), with the exact intra-chunk inverse (I + A)^-1 (the reference's solve loop,
+ * :271-292, is only first-order accurate).  dk = dv = 128, chunk = 64.  ws must hold
+ * tsa_gdn_chunked_workspace_bytes(...) bytes of device memory. */
+size_t tsa_gdn_chunked_workspace_bytes(int B, int T, int Hq, int Hv, int dk, int dv,
+                                       int chunk);
+int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v, const float* g_log,
+                        const float* beta, float* state, void* out, int B, int T, int Hq,
+                        int Hv, int dk, int dv, int chunk, float scale, void* ws,
+                        size_t ws_bytes, void* stream);
+
+/* Token-serial Gated DeltaNet over T tokens (state held on chip for all T).  Replaces the
+ * token-serial kernels gdn_serial_kernel, gdn_smem_kernel, gdn_occ/occ2/occ4/occ4p/occ8
+ * (src/gdn_sm75.cu:57-188,577-893).  dk = dv = 128. */
+int tsa_gdn_recurrent_fwd(const void* q, const void* k, const void* v, const float* g_log,
+                          const float* beta, float* state, void* out, int B, int T, int Hq,
+                          int Hv, int dk, int dv, float scale, void* stream);
+
+/* One decode step: one token for each of B sequences, q/k [B][Hq][dk], v/out [B][Hv][dv],
+ * g_log/beta [B][Hv], state [B][Hv][dv][dk] updated in place.  The T = 1 case of the
+ * token-serial kernels (src/gdn_sm75.cu:744-784 with one iteration). */
+int tsa_gdn_decode_step(const void* q, const void* k, const void* v, const float* g_log,
+                        const float* beta, float* state, void* out, int B, int Hq, int Hv,
+                        int dk, int dv, float scale, void* stream);
+
+/* The lab's naive GDN check on the device: one thread per state column, fp32, state read
+ * and written in global memory, the order of gdn_cpu (src/gdn_sm75.cu:1078-1106) and
+ * gdn_serial_kernel (:57-92).  Used by the gdn driver's error check.  Any dk, dv >= 1. */
+int tsa_gdn_naive(const void* q, const void* k, const void* v, const float* g_log,
+                  const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
+                  int dk, int dv, float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

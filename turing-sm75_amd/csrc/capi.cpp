@@ -1,0 +1,127 @@
+// capi.cpp -- the extern "C" boundary declared in include/tsa.h.
+//
+// Validation happens here, before any HIP call, so argument errors are reported the same
+// way on machines without a GPU.  The launch functions in kernels.h assume valid input.
+#include <climits>
+#include <cmath>
+
+#include "../../include/tsa.h"
+#include "kernels.h"
+
+namespace {
+
+inline int from_hip(hipError_t e) { return e == hipSuccess ? TSA_OK : TSA_ERR_LAUNCH; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// a * b * c fits in an int (workgroup counts and per-dimension products).
+inline bool fits_int(long long a, long long b, long long c = 1) {
+    return a >= 0 && b >= 0 && c >= 0 && a * b <= INT_MAX && a * b * c <= INT_MAX;
+}
+
+int check_attn(const void* q, const void* k, const void* v, const void* o, int B, int H, int S,
+               int D, float scale, int causal) {
+    if (!q || !k || !v || !o) return TSA_ERR_NULL;
+    if (B < 1 || H < 1 || S < 1 || D < 1) return TSA_ERR_SHAPE;
+    if (D != 64 && D != 128) return TSA_ERR_UNSUPPORTED;
+    if (causal != 0 && causal != 1) return TSA_ERR_ARG;
+    // The running max is taken over raw q.k, which is the max of the scaled scores only
+    // for scale > 0 (the reference's scale is 1/sqrt(D), src/attn_sm75.cu:462).
+    if (!(scale > 0.f) || !std::isfinite(scale)) return TSA_ERR_ARG;
+    // workgroups: B*H*ceil(S/128) for the MFMA kernel, B*H*S/128 for the naive one
+    if (!fits_int(B, H, S)) return TSA_ERR_SHAPE;
+    return TSA_OK;
+}
+
+int check_gdn(const void* q, const void* k, const void* v, const float* g, const float* beta,
+              const float* state, const void* out, int B, int T, int Hq, int Hv, int dk, int dv,
+              float scale) {
+    if (!q || !k || !v || !g || !beta || !state || !out) return TSA_ERR_NULL;
+    if (B < 1 || T < 1 || Hq < 1 || Hv < 1 || dk < 1 || dv < 1) return TSA_ERR_SHAPE;
+    if (!std::isfinite(scale)) return TSA_ERR_ARG;
+    // element offsets are 64-bit in every kernel; only workgroup counts must fit an int
+    if (!fits_int(B, Hv, dv)) return TSA_ERR_SHAPE;
+    return TSA_OK;
+}
+
+}  // namespace
+
+extern "C" const char* tsa_strerror(int code) {
+    switch (code) {
+        case TSA_OK: return "ok";
+        case TSA_ERR_NULL: return "a required pointer is NULL";
+        case TSA_ERR_SHAPE: return "invalid shape (size < 1, too large, or inconsistent)";
+        case TSA_ERR_UNSUPPORTED: return "shape not supported by this build (attention: D in {64,128}; GDN: dk = dv = 128, chunk = 64)";
+        case TSA_ERR_WORKSPACE: return "workspace is NULL or smaller than the required size";
+        case TSA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
+        case TSA_ERR_ARG: return "invalid argument (causal not 0/1, or scale not finite / not > 0)";
+        default: return "unknown tsa error code";
+    }
+}
+
+extern "C" const char* tsa_version(void) { return "tsa 0.1 gfx950"; }
+
+extern "C" int tsa_attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H,
+                            int S, int D, float scale, int causal, void* stream) {
+    const int rc = check_attn(q, k, v, o, B, H, S, D, scale, causal);
+    if (rc) return rc;
+    return from_hip(tsa::attn_fwd(q, k, v, o, B, H, S, D, scale, causal, as_stream(stream)));
+}
+
+extern "C" int tsa_attn_naive(const void* q, const void* k, const void* v, void* o, int B,
+                              int H, int S, int D, float scale, int causal, void* stream) {
+    const int rc = check_attn(q, k, v, o, B, H, S, D, scale, causal);
+    if (rc) return rc;
+    return from_hip(tsa::attn_naive(q, k, v, o, B, H, S, D, scale, causal, as_stream(stream)));
+}
+
+extern "C" size_t tsa_gdn_chunked_workspace_bytes(int B, int T, int Hq, int Hv, int dk, int dv,
+                                                  int chunk) {
+    if (B < 1 || T < 1 || Hq < 1 || Hv < 1 || dk != 128 || dv != 128 || chunk != 64) return 0;
+    return tsa::gdn_chunked_ws_bytes(B, T, Hv);
+}
+
+extern "C" int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v,
+                                   const float* g_log, const float* beta, float* state, void* out,
+                                   int B, int T, int Hq, int Hv, int dk, int dv, int chunk,
+                                   float scale, void* ws, size_t ws_bytes, void* stream) {
+    int rc = check_gdn(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale);
+    if (rc) return rc;
+    if (chunk < 1) return TSA_ERR_SHAPE;
+    if (dk != 128 || dv != 128 || chunk != 64) return TSA_ERR_UNSUPPORTED;
+    const long long nch = (T + 63LL) / 64;
+    if (!fits_int(B, Hv, nch) || !fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
+    const size_t need = tsa::gdn_chunked_ws_bytes(B, T, Hv);
+    if (!ws || ws_bytes < need) return TSA_ERR_WORKSPACE;
+    return from_hip(tsa::gdn_chunked(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale, ws,
+                                     as_stream(stream)));
+}
+
+extern "C" int tsa_gdn_recurrent_fwd(const void* q, const void* k, const void* v,
+                                     const float* g_log, const float* beta, float* state,
+                                     void* out, int B, int T, int Hq, int Hv, int dk, int dv,
+                                     float scale, void* stream) {
+    int rc = check_gdn(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale);
+    if (rc) return rc;
+    if (dk != 128 || dv != 128) return TSA_ERR_UNSUPPORTED;
+    if (!fits_int(B, Hv, 4)) return TSA_ERR_SHAPE;
+    return from_hip(tsa::gdn_recurrent(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale,
+                                       as_stream(stream)));
+}
+
+extern "C" int tsa_gdn_decode_step(const void* q, const void* k, const void* v,
+                                   const float* g_log, const float* beta, float* state, void* out,
+                                   int B, int Hq, int Hv, int dk, int dv, float scale,
+                                   void* stream) {
+    return tsa_gdn_recurrent_fwd(q, k, v, g_log, beta, state, out, B, 1, Hq, Hv, dk, dv, scale,
+                                 stream);
+}
+
+extern "C" int tsa_gdn_naive(const void* q, const void* k, const void* v, const float* g_log,
+                             const float* beta, float* state, void* out, int B, int T, int Hq,
+                             int Hv, int dk, int dv, float scale, void* stream) {
+    int rc = check_gdn(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale);
+    if (rc) return rc;
+    return from_hip(tsa::gdn_naive(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv,
+                                   scale, as_stream(stream)));
+}

@@ -1,0 +1,56 @@
+// common.h -- shared device helpers for the gfx950 kernels (CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tsa {
+
+typedef _Float16 half_t;
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// D(32x32 fp32) += A(32x16 fp16) * B(16x32 fp16).  Lane l holds A[l%32][8*(l/32)+s] and
+// B[8*(l/32)+s][l%32] in slot s, and D[8*(r/4) + 4*(l/32) + r%4][l%32] in register r.
+__device__ __forceinline__ float16_t mfma32(const half8_t& a, const half8_t& b, const float16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+// D(16x16 fp32) += A(16x32 fp16) * B(32x16 fp16).  Lane l holds A[l%16][8*(l/16)+s],
+// B[8*(l/16)+s][l%16] in slot s, and D[4*(l/16) + r][l%16] in register r.
+__device__ __forceinline__ float4_t mfma16(const half8_t& a, const half8_t& b, const float4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Transposing LDS read (ds_read_b64_tr_b16).  Within each group of 16 lanes, source lane
+// s supplies the address of 4 consecutive fp16 values; result lane i, slot j receives
+// element i%4 of source lane 4*j + i/4.
+__device__ __forceinline__ half4_t lds_read_tr16(const half_t* p) {
+    typedef __attribute__((address_space(3))) fp16x4_t* lds_ptr_t;
+    fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_ptr_t)(p));
+    return __builtin_bit_cast(half4_t, v);
+}
+
+// DPP lane moves within a row of 16 lanes (row_mask / bank_mask all enabled).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <- lane 7-i within each group of 8
+
+// Sum over each aligned group of 8 lanes; every lane of the group receives the total.
+__device__ __forceinline__ float sum8(float x) {
+    x += dpp_mov<kDppXor1>(x);
+    x += dpp_mov<kDppXor2>(x);
+    x += dpp_mov<kDppHalfMirror>(x);
+    return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace tsa

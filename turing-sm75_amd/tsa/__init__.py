@@ -1,0 +1,221 @@
+"""ctypes binding of libtsa.so, the C-ABI declared in include/tsa.h, for torch tensors.
+
+torch is only plumbing here (device memory and the current HIP stream); every call goes
+straight to the hand-written gfx950 kernels.  There is no fallback: if the library is
+missing or a call fails, an exception is raised.
+
+Shapes and dtypes mirror the reference labs (cookys/turing-sm75):
+  attention  q, k, v, o      [B, H, S, D] fp16                (src/attn_sm75.cu:64,254)
+  GDN        q, k            [B, T, Hq, dk] fp16              (src/gdn_sm75.cu:75-77)
+             v, out          [B, T, Hv, dv] fp16
+             g_log, beta     [B, T, Hv] fp32
+             state           [B, Hv, dv, dk] fp32, updated in place (:71-72,1094)
+  decode     q, k [B, Hq, dk], v/out [B, Hv, dv], g_log/beta [B, Hv]
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import re
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.dirname(_HERE)
+LIB_PATH = os.path.join(PKG_ROOT, "lib", "libtsa.so")
+HEADER_PATH = os.path.join(os.path.dirname(PKG_ROOT), "include", "tsa.h")
+
+TSA_OK = 0
+TSA_ERR_NULL = 1
+TSA_ERR_SHAPE = 2
+TSA_ERR_UNSUPPORTED = 3
+TSA_ERR_WORKSPACE = 4
+TSA_ERR_LAUNCH = 5
+TSA_ERR_ARG = 6
+
+_vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+_SIGNATURES = {
+    "tsa_strerror": (ctypes.c_char_p, [_i]),
+    "tsa_version": (ctypes.c_char_p, []),
+    "tsa_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp]),
+    "tsa_attn_naive": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp]),
+    "tsa_gdn_chunked_workspace_bytes": (_sz, [_i] * 7),
+    "tsa_gdn_chunked_fwd": (_i, [_vp] * 7 + [_i] * 8 + [_f, _vp, _sz, _vp]),
+    "tsa_gdn_recurrent_fwd": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp]),
+    "tsa_gdn_decode_step": (_i, [_vp] * 7 + [_i] * 5 + [_f, _vp]),
+    "tsa_gdn_naive": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp]),
+}
+
+
+class TsaError(RuntimeError):
+    """A tsa_* entry point returned a non-zero code."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"tsa error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libtsa.so once (raises OSError with a build hint when it is missing)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise OSError(f"{path} not found: build it with `make -C turing-sm75_amd` "
+                          "(or __graft_entry__.build())")
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def header_symbols(path: str = HEADER_PATH) -> list[str]:
+    """Names of the functions include/tsa.h declares."""
+    text = open(path).read()
+    return sorted(set(re.findall(r"\b(tsa_[a-z0-9_]+)\s*\(", text)))
+
+
+def strerror(code: int) -> str:
+    return load().tsa_strerror(code).decode()
+
+
+def _check(code: int) -> None:
+    if code != TSA_OK:
+        raise TsaError(code, strerror(code))
+
+
+def _stream(stream):
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _need(t, dtype, ndim, name):
+    import torch
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype != dtype or t.dim() != ndim or not t.is_cuda or not t.is_contiguous():
+        raise ValueError(f"{name}: expected a contiguous {ndim}-d {dtype} CUDA tensor, got "
+                         f"{tuple(t.shape)} {t.dtype} on {t.device}")
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+# ---------------------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------------------
+def attn_fwd(q, k, v, out=None, scale=None, causal=True, stream=None, naive=False):
+    """O = softmax(scale Q K^T [+ causal mask]) V on the MFMA kernel (or the naive one)."""
+    import torch
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _need(t, torch.float16, 4, name)
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    B, H, S, D = q.shape
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.float16, 4, "out")
+    if out.shape != q.shape:
+        raise ValueError("out shape differs from q")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    fn = load().tsa_attn_naive if naive else load().tsa_attn_fwd
+    _check(fn(_ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, S, D, float(scale), int(bool(causal)),
+              _stream(stream)))
+    return out
+
+
+# ---------------------------------------------------------------------------------------
+# Gated DeltaNet
+# ---------------------------------------------------------------------------------------
+def _gdn_shapes(q, k, v, g_log, beta, state, batched_t: bool):
+    import torch
+    nd = 4 if batched_t else 3
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _need(t, torch.float16, nd, name)
+    _need(g_log, torch.float32, nd - 1, "g_log")
+    _need(beta, torch.float32, nd - 1, "beta")
+    _need(state, torch.float32, 4, "state")
+    if batched_t:
+        B, T, Hq, dk = q.shape
+        Hv, dv = v.shape[2], v.shape[3]
+        ok = (k.shape == q.shape and v.shape[:2] == (B, T) and g_log.shape == (B, T, Hv)
+              and beta.shape == (B, T, Hv) and state.shape == (B, Hv, dv, dk))
+    else:
+        B, Hq, dk = q.shape
+        Hv, dv = v.shape[1], v.shape[2]
+        T = 1
+        ok = (k.shape == q.shape and v.shape[0] == B and g_log.shape == (B, Hv)
+              and beta.shape == (B, Hv) and state.shape == (B, Hv, dv, dk))
+    if not ok:
+        raise ValueError("inconsistent GDN shapes: q %s k %s v %s g %s beta %s state %s" % (
+            tuple(q.shape), tuple(k.shape), tuple(v.shape), tuple(g_log.shape),
+            tuple(beta.shape), tuple(state.shape)))
+    return B, T, Hq, Hv, dk, dv
+
+
+def gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk=128, dv=128, chunk=64) -> int:
+    return int(load().tsa_gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk))
+
+
+def gdn_chunked_fwd(q, k, v, g_log, beta, state, out=None, scale=None, chunk=64, ws=None,
+                    stream=None):
+    """Chunked prefill; state [B, Hv, dv, dk] is updated in place; returns out."""
+    import torch
+    B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, True)
+    if out is None:
+        out = torch.empty_like(v)
+    _need(out, torch.float16, 4, "out")
+    if scale is None:
+        scale = 1.0 / math.sqrt(dk)
+    need = gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk)
+    if ws is None:
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    _check(load().tsa_gdn_chunked_fwd(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(g_log), _ptr(beta), _ptr(state), _ptr(out),
+        B, T, Hq, Hv, dk, dv, chunk, float(scale), _ptr(ws), ws.numel() * ws.element_size(),
+        _stream(stream)))
+    return out
+
+
+def gdn_recurrent_fwd(q, k, v, g_log, beta, state, out=None, scale=None, stream=None,
+                      naive=False):
+    """Token-serial recurrence over T tokens (or the naive check kernel); state in place."""
+    import torch
+    B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, True)
+    if out is None:
+        out = torch.empty_like(v)
+    _need(out, torch.float16, 4, "out")
+    if scale is None:
+        scale = 1.0 / math.sqrt(dk)
+    fn = load().tsa_gdn_naive if naive else load().tsa_gdn_recurrent_fwd
+    _check(fn(_ptr(q), _ptr(k), _ptr(v), _ptr(g_log), _ptr(beta), _ptr(state), _ptr(out),
+              B, T, Hq, Hv, dk, dv, float(scale), _stream(stream)))
+    return out
+
+
+def gdn_decode_step(q, k, v, g_log, beta, state, out=None, scale=None, stream=None):
+    """One token per sequence: q/k [B, Hq, dk], v [B, Hv, dv]; state in place."""
+    import torch
+    B, _, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, False)
+    if out is None:
+        out = torch.empty_like(v)
+    _need(out, torch.float16, 3, "out")
+    if scale is None:
+        scale = 1.0 / math.sqrt(dk)
+    _check(load().tsa_gdn_decode_step(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(g_log), _ptr(beta), _ptr(state), _ptr(out),
+        B, Hq, Hv, dk, dv, float(scale), _stream(stream)))
+    return out
+
+
+def gdn_naive(q, k, v, g_log, beta, state, out=None, scale=None, stream=None):
+    """The naive on-device check kernel (one thread per state column)."""
+    return gdn_recurrent_fwd(q, k, v, g_log, beta, state, out, scale, stream, naive=True)
