@@ -1,0 +1,338 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention + Gated DeltaNet hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--decode-steps N]
+
+One bench step is one pass over the hot path with every input already resident in HBM:
+  * attention forward, B=1 H=32 S=8192 D=128 causal, fp16, N(0, 0.5) with 1% of the
+    entries x8 (outlier stress), fp32 softmax statistics;
+  * chunked Gated DeltaNet prefill, B=1 T=4096 Hq=16 Hv=32 dk=dv=128 C=64, fp16 q/k/v
+    (q, k rows L2-normalised), beta = sigmoid(N(0,1)), g_log = -softplus(N(0,1)), fp32
+    state from zero;
+  * one Gated DeltaNet decode step for 16 sequences x 32 V-heads (128x128 fp32 state each,
+    N(0, 0.02)), cycling through 16 state replicas (512 MiB > the 256 MiB Infinity Cache)
+    so every step streams its state from HBM.
+W untimed warmup steps, then exactly K timed steps between two synchronisations.  Each
+kernel's average duration comes from HIP events recorded on the stream it runs on.
+
+Printed: one JSON line.  `value` is the attention forward throughput (TFLOP/s, causal
+executed FLOPs 2*B*H*S*(S+1)*D, the convention of src/attn_sm75.cu:534), the kernel that
+dominates the step; `parts` carries all three components, each with its absolute
+throughput, its roofline fraction and a CPU baseline (the oracle, timed on a bounded
+sample on this machine's host cores).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "turing-sm75_amd"))
+
+PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA (no sparsity)
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+
+# configuration of each part
+ATTN = dict(B=1, H=32, S=8192, D=128, causal=True)
+PREFILL = dict(B=1, T=4096, Hq=16, Hv=32, d=128, chunk=64)
+DECODE = dict(B=16, Hq=16, Hv=32, d=128, replicas=16)
+
+
+def attn_flops(B, H, S, D, causal, **_):
+    return 2.0 * B * H * S * (S + 1) * D if causal else 4.0 * B * H * S * S * D
+
+
+def prefill_flops(B, T, Hq, Hv, d, chunk, **_):
+    # per (head, chunk), full (not triangle-halved) products:
+    # K K^T, Q K^T, Tm K, Tm V, (M.QK^T) Vnew, W S, Q S, K^T Vnew
+    nch = math.ceil(T / chunk)
+    per = 2 * chunk * (chunk * (3 * d + 2 * d) + 3 * d * d)
+    return float(B * Hv * nch * per)
+
+
+def prefill_bytes(B, T, Hq, Hv, d, **_):
+    return float(2 * B * T * Hq * d * 2 + 2 * B * T * Hv * d * 2 + 2 * B * T * Hv * 4
+                 + 2 * B * Hv * d * d * 4)
+
+
+def decode_bytes(B, Hq, Hv, d, **_):
+    return float(2 * B * Hv * d * d * 4 + 2 * B * Hq * d * 2 + B * Hv * d * 2 + 2 * B * Hv * 4
+                 + B * Hv * d * 2)
+
+
+def omp_threads():
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
+
+
+def load_traffic():
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by a
+    copy-kernel calibration), committed in profiles/traffic.json; None when absent."""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(p):
+        return {}
+    with open(p) as f:
+        return json.load(f)
+
+
+def make_inputs(torch, dev, seed=2026):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+
+    def attn_tensor():
+        s = ATTN
+        x = 0.5 * torch.randn(s["B"], s["H"], s["S"], s["D"], device=dev, generator=gen)
+        x = torch.where(torch.rand(x.shape, device=dev, generator=gen) < 0.01, 8 * x, x)
+        return x.half().contiguous()
+
+    def l2n(x):
+        return x / x.norm(dim=-1, keepdim=True)
+
+    a = {n: attn_tensor() for n in ("q", "k", "v")}
+    a["o"] = torch.empty_like(a["q"])
+
+    p = PREFILL
+    pre = dict(
+        q=l2n(torch.randn(p["B"], p["T"], p["Hq"], p["d"], device=dev, generator=gen)).half(),
+        k=l2n(torch.randn(p["B"], p["T"], p["Hq"], p["d"], device=dev, generator=gen)).half(),
+        v=torch.randn(p["B"], p["T"], p["Hv"], p["d"], device=dev, generator=gen).half(),
+        beta=torch.sigmoid(torch.randn(p["B"], p["T"], p["Hv"], device=dev, generator=gen)),
+        g=-torch.nn.functional.softplus(torch.randn(p["B"], p["T"], p["Hv"], device=dev, generator=gen)),
+    )
+    pre["state"] = torch.zeros(p["B"], p["Hv"], p["d"], p["d"], device=dev)
+    pre["out"] = torch.empty_like(pre["v"])
+
+    d = DECODE
+    dec = dict(
+        q=l2n(torch.randn(d["B"], d["Hq"], d["d"], device=dev, generator=gen)).half(),
+        k=l2n(torch.randn(d["B"], d["Hq"], d["d"], device=dev, generator=gen)).half(),
+        v=torch.randn(d["B"], d["Hv"], d["d"], device=dev, generator=gen).half(),
+        beta=torch.sigmoid(torch.randn(d["B"], d["Hv"], device=dev, generator=gen)),
+        g=-torch.nn.functional.softplus(torch.randn(d["B"], d["Hv"], device=dev, generator=gen)),
+    )
+    dec["states"] = [0.02 * torch.randn(d["B"], d["Hv"], d["d"], d["d"], device=dev, generator=gen)
+                     for _ in range(d["replicas"])]
+    dec["out"] = torch.empty_like(dec["v"])
+    return a, pre, dec
+
+
+def cpu_baselines(torch, a, pre, dec, threads):
+    """Time the oracle (the reference's naive paths restated in C++) on bounded samples."""
+    import numpy as np
+    import oracle
+    res = {}
+    # attention: every row of 2 of the 32 heads (causal), all host threads
+    s = ATTN
+    nh = 2
+    q, k, v = (a[n][:, :nh].cpu().numpy() for n in ("q", "k", "v"))
+    rows = np.arange(nh * s["S"], dtype=np.int64)
+    t0 = time.perf_counter()
+    oracle.attn_rows(q, k, v, rows, True, nthreads=threads)
+    dt = time.perf_counter() - t0
+    fl = attn_flops(1, nh, s["S"], s["D"], True)
+    res["attn_fwd"] = {"value": fl / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                       "sample": f"all {s['S']} causal rows of {nh} of {s['H']} heads ({dt:.1f} s)"}
+    # prefill: serial recurrence, all 4096 tokens of 8 of the 32 V-heads
+    p = PREFILL
+    hv_s = 8
+    g = lambda n: pre[n].float().cpu().numpy()
+    qn, kn = g("q")[:, :, :hv_s], g("k")[:, :, :hv_s]  # V-heads 0..7 read QK heads 0..7
+    vn, bn, gn = g("v")[:, :, :hv_s], g("beta")[:, :, :hv_s], g("g")[:, :, :hv_s]
+    st = np.zeros((1, hv_s, p["d"], p["d"]), np.float32)
+    t0 = time.perf_counter()
+    oracle.gdn_serial(qn, kn, vn, gn, bn, st, nthreads=threads)
+    dt = time.perf_counter() - t0
+    tok_s = p["B"] * p["T"] / (dt * p["Hv"] / hv_s)
+    res["gdn_prefill"] = {"value": tok_s, "unit": "tok/s", "cores": threads, "kind": "port",
+                          "sample": f"T={p['T']} for {hv_s} of {p['Hv']} V-heads ({dt:.1f} s), scaled to all heads"}
+    # decode: 64 single-token steps over the full 16 x 32-head state
+    d = DECODE
+    steps = 64
+    qd, kd, vd = (dec[n].float().cpu().numpy()[:, None] for n in ("q", "k", "v"))
+    bd, gd = (dec[n].cpu().numpy()[:, None] for n in ("beta", "g"))
+    st = dec["states"][0].cpu().numpy()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, st = oracle.gdn_serial(qd, kd, vd, gd, bd, st, nthreads=threads)
+    dt = time.perf_counter() - t0
+    res["gdn_decode"] = {"value": decode_bytes(**d) * steps / dt / 1e9, "unit": "GB/s", "cores": threads,
+                         "kind": "port", "sample": f"{steps} steps of 16 sequences x 32 heads ({dt:.1f} s)"}
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--decode-steps", type=int, default=512,
+                    help="length of the extra decode-only run (the 512-step workload)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the hot path's sharding (heads / sequences) is "
+              "described in DESIGN.md and no multi-GPU figure is produced", file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import torch
+    import tsa
+    tsa.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    a, pre, dec = make_inputs(torch, dev)
+    ws = torch.empty(tsa.gdn_chunked_workspace_bytes(PREFILL["B"], PREFILL["T"], PREFILL["Hq"],
+                                                     PREFILL["Hv"]), dtype=torch.uint8, device=dev)
+    step_no = [0]
+
+    def attn():
+        tsa.attn_fwd(a["q"], a["k"], a["v"], a["o"], causal=True, stream=stream)
+
+    def prefill():
+        pre["state"].zero_()  # each step is the same prefill from a zero state
+        tsa.gdn_chunked_fwd(pre["q"], pre["k"], pre["v"], pre["g"], pre["beta"], pre["state"],
+                            pre["out"], ws=ws, stream=stream)
+
+    def decode():
+        st = dec["states"][step_no[0] % DECODE["replicas"]]
+        tsa.gdn_decode_step(dec["q"], dec["k"], dec["v"], dec["g"], dec["beta"], st, dec["out"],
+                            stream=stream)
+
+    parts = [("attn_fwd", attn), ("gdn_prefill", prefill), ("gdn_decode", decode)]
+    for _ in range(args.warmup):
+        for _, fn in parts:
+            fn()
+        step_no[0] += 1
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in parts] for _ in range(K)]
+    zero_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(K)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(K):
+        for j, (name, fn) in enumerate(parts):
+            if name == "gdn_prefill":  # time the state reset separately, it is not the kernel
+                zero_ev[i][0].record(stream)
+                pre["state"].zero_()
+                zero_ev[i][1].record(stream)
+                ev[i][j][0].record(stream)
+                tsa.gdn_chunked_fwd(pre["q"], pre["k"], pre["v"], pre["g"], pre["beta"],
+                                    pre["state"], pre["out"], ws=ws, stream=stream)
+                ev[i][j][1].record(stream)
+            else:
+                ev[i][j][0].record(stream)
+                fn()
+                ev[i][j][1].record(stream)
+        step_no[0] += 1
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = {name: sum(ev[i][j][0].elapsed_time(ev[i][j][1]) for i in range(K)) / K
+          for j, (name, _) in enumerate(parts)}
+    ms_step = wall * 1e3 / K
+
+    # decode-only runs: the 512-step workload cycling replicas, and one resident buffer
+    n = args.decode_steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(n):
+        tsa.gdn_decode_step(dec["q"], dec["k"], dec["v"], dec["g"], dec["beta"],
+                            dec["states"][i % DECODE["replicas"]], dec["out"], stream=stream)
+    e1.record(stream)
+    e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e2.record(stream)
+    for i in range(n):
+        tsa.gdn_decode_step(dec["q"], dec["k"], dec["v"], dec["g"], dec["beta"],
+                            dec["states"][0], dec["out"], stream=stream)
+    e3.record(stream)
+    torch.cuda.synchronize()
+    dec_rot_ms = e0.elapsed_time(e1) / n
+    dec_res_ms = e2.elapsed_time(e3) / n
+
+    finite = bool(torch.isfinite(a["o"]).all() and torch.isfinite(pre["out"]).all()
+                  and torch.isfinite(pre["state"]).all() and torch.isfinite(dec["out"]).all())
+
+    traffic = load_traffic()
+    fa = attn_flops(**ATTN)
+    fp = prefill_flops(**PREFILL)
+    bp = prefill_bytes(**PREFILL)
+    bd = decode_bytes(**DECODE)
+    attn_tflops = fa / (ms["attn_fwd"] * 1e-3) / 1e12
+    pre_tflops = fp / (ms["gdn_prefill"] * 1e-3) / 1e12
+    dec_gbs = bd / (ms["gdn_decode"] * 1e-3) / 1e9
+
+    def roof(bound, achieved, peak, unit, key):
+        return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                "frac": round(achieved / peak, 4), "traffic": traffic.get(key)}
+
+    out_parts = {
+        "attn_fwd": {
+            "workload": "attention fwd B=1 H=32 S=8192 D=128 causal fp16, N(0,0.5) + 1% x8 outliers",
+            "value": round(attn_tflops, 2), "unit": "TFLOP/s", "ms": round(ms["attn_fwd"], 5),
+            "flop_per_launch": fa,
+            "roofline": roof("mfma", attn_tflops, PEAK_MFMA_F16_TFLOPS, "TFLOP/s", "attn_fwd"),
+        },
+        "gdn_prefill": {
+            "workload": "chunked GDN prefill B=1 T=4096 Hq=16 Hv=32 d=128 C=64, fp16 I/O, fp32 state",
+            "value": round(PREFILL["B"] * PREFILL["T"] / (ms["gdn_prefill"] * 1e-3), 1),
+            "unit": "tok/s", "ms": round(ms["gdn_prefill"], 5), "flop_per_launch": fp,
+            "bytes_per_launch": bp,
+            "roofline": roof("mfma", pre_tflops, PEAK_MFMA_F16_TFLOPS, "TFLOP/s", "gdn_prefill"),
+            "hbm_frac": round(bp / (ms["gdn_prefill"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        },
+        "gdn_decode": {
+            "workload": "GDN decode step, 16 sequences x 32 V-heads, 128x128 fp32 state, 16 replicas cycled",
+            "value": round(dec_gbs, 1), "unit": "GB/s", "ms": round(ms["gdn_decode"], 5),
+            "bytes_per_launch": bd,
+            "tok_s": round(DECODE["B"] / (ms["gdn_decode"] * 1e-3), 1),
+            "roofline": roof("hbm", dec_gbs, PEAK_HBM_GBS, "GB/s", "gdn_decode"),
+            "decode_only_512": {"ms_per_step_replicas": round(dec_rot_ms, 5),
+                                "gbs_replicas": round(bd / (dec_rot_ms * 1e-3) / 1e9, 1),
+                                "ms_per_step_resident": round(dec_res_ms, 5),
+                                "gbs_resident_in_cache": round(bd / (dec_res_ms * 1e-3) / 1e9, 1)},
+        },
+    }
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baselines(torch, a, pre, dec, omp_threads())
+        for k, v in cpu.items():
+            out_parts[k]["cpu_baseline"] = {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                                            for kk, vv in v.items()}
+
+    line = {
+        "metric": "attn fwd TFLOP/s + GDN prefill tok/s + decode GB/s, % of MI355X roofline",
+        "value": round(attn_tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded torch generators on the device)",
+        "config": {"workload": "attention fwd B=1 H=32 S=8192 D=128 causal + chunked GDN prefill "
+                               "B=1 T=4096 Hq=16 Hv=32 C=64 + GDN decode step B=16 Hv=32",
+                   "parallelism": "single GPU"},
+        "roofline": out_parts["attn_fwd"]["roofline"],
+        "cpu_baseline": out_parts["attn_fwd"].get("cpu_baseline"),
+        "parts": out_parts,
+        "outputs_finite": finite,
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if finite else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,104 @@
+"""C-ABI surface on CPU: the library loads, exports every function include/tsa.h declares,
+and rejects invalid arguments with the documented codes before touching the GPU.
+The lab drivers reject bad command lines with exit code 2 (src/attn_sm75.cu:449-460,
+src/gdn_sm75.cu:1249-1252)."""
+import ctypes
+import os
+import subprocess
+
+import pytest
+
+import tsa
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "turing-sm75_amd", "bin")
+NULL = None
+DUMMY = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation
+
+
+def test_exports_every_declared_symbol():
+    lib = tsa.load()
+    names = tsa.header_symbols()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), n
+    out = subprocess.run(["nm", "-D", "--defined-only", tsa.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert set(names) <= exported
+
+
+def test_version_and_strerror():
+    lib = tsa.load()
+    assert lib.tsa_version().decode().startswith("tsa ")
+    for code in range(7):
+        assert tsa.strerror(code)
+    assert "unknown" in tsa.strerror(99)
+
+
+def _attn(*, q=DUMMY, B=1, H=1, S=16, D=128, scale=0.1, causal=1):
+    return tsa.load().tsa_attn_fwd(q, DUMMY, DUMMY, DUMMY, B, H, S, D, scale, causal, NULL)
+
+
+def test_attn_argument_errors():
+    assert _attn(q=NULL) == tsa.TSA_ERR_NULL
+    assert _attn(S=0) == tsa.TSA_ERR_SHAPE
+    assert _attn(B=-1) == tsa.TSA_ERR_SHAPE
+    assert _attn(D=96) == tsa.TSA_ERR_UNSUPPORTED
+    assert _attn(D=256) == tsa.TSA_ERR_UNSUPPORTED
+    assert _attn(causal=2) == tsa.TSA_ERR_ARG
+    assert _attn(scale=0.0) == tsa.TSA_ERR_ARG
+    assert _attn(scale=-0.1) == tsa.TSA_ERR_ARG
+    assert _attn(scale=float("nan")) == tsa.TSA_ERR_ARG
+    assert _attn(B=1 << 16, H=1 << 16, S=1) == tsa.TSA_ERR_SHAPE
+    lib = tsa.load()
+    assert lib.tsa_attn_naive(DUMMY, DUMMY, NULL, DUMMY, 1, 1, 4, 64, 0.1, 0, NULL) == tsa.TSA_ERR_NULL
+
+
+def _chunked(*, T=64, Hv=2, dk=128, dv=128, chunk=64, ws=DUMMY, ws_bytes=1 << 30, st=DUMMY):
+    return tsa.load().tsa_gdn_chunked_fwd(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, st, DUMMY,
+                                          1, T, 1, Hv, dk, dv, chunk, 0.1, ws, ws_bytes, NULL)
+
+
+def test_gdn_chunked_argument_errors():
+    need = tsa.gdn_chunked_workspace_bytes(1, 64, 1, 2)
+    assert need > 0
+    assert _chunked(st=NULL) == tsa.TSA_ERR_NULL
+    assert _chunked(T=0) == tsa.TSA_ERR_SHAPE
+    assert _chunked(dk=64, dv=64) == tsa.TSA_ERR_UNSUPPORTED
+    assert _chunked(chunk=16) == tsa.TSA_ERR_UNSUPPORTED
+    assert _chunked(chunk=0) == tsa.TSA_ERR_SHAPE
+    assert _chunked(ws=NULL) == tsa.TSA_ERR_WORKSPACE
+    assert _chunked(ws_bytes=need - 1) == tsa.TSA_ERR_WORKSPACE
+
+
+def test_gdn_workspace_bytes_scales_with_chunks():
+    a = tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32)
+    assert tsa.gdn_chunked_workspace_bytes(1, 65, 16, 32) == 2 * a
+    assert tsa.gdn_chunked_workspace_bytes(2, 4096, 16, 32) == 2 * 64 * a
+    assert tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32, dk=64) == 0
+    assert tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32, chunk=32) == 0
+
+
+def test_gdn_recurrent_and_decode_argument_errors():
+    lib = tsa.load()
+    args = [DUMMY] * 7
+    assert lib.tsa_gdn_recurrent_fwd(*args, 1, 4, 1, 2, 128, 64, 0.1, NULL) == tsa.TSA_ERR_UNSUPPORTED
+    assert lib.tsa_gdn_recurrent_fwd(*args, 1, 0, 1, 2, 128, 128, 0.1, NULL) == tsa.TSA_ERR_SHAPE
+    assert lib.tsa_gdn_decode_step(*args[:6], NULL, 4, 1, 2, 128, 128, 0.1, NULL) == tsa.TSA_ERR_NULL
+    assert lib.tsa_gdn_decode_step(*args, 4, 1, 2, 128, 128, float("inf"), NULL) == tsa.TSA_ERR_ARG
+    assert lib.tsa_gdn_naive(*args, 1, 1, 0, 2, 128, 128, 0.1, NULL) == tsa.TSA_ERR_SHAPE
+
+
+@pytest.mark.parametrize("argv", [
+    ["attn_sm75", "1", "2", "3"],
+    ["attn_sm75", "1", "2", "64", "96"],
+    ["attn_sm75", "--causal"],
+    ["gdn", "0"],
+    ["gdn", "64", "--mode", "train"],
+])
+def test_drivers_usage_errors_exit_2(argv):
+    exe = os.path.join(BIN, argv[0])
+    assert os.path.exists(exe), "build the drivers first (make -C turing-sm75_amd)"
+    r = subprocess.run([exe] + argv[1:], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2, (r.returncode, r.stdout, r.stderr)

@@ -1,0 +1,171 @@
+"""GPU parity: chunked (tsa_gdn_chunked_fwd), token-serial (tsa_gdn_recurrent_fwd), decode
+(tsa_gdn_decode_step) and naive (tsa_gdn_naive) Gated DeltaNet kernels against the oracle.
+
+Gates: outputs max-abs < 0.02 (fp16 I/O, src/gdn_sm75.cu:1313) and the fp32 state within
+1e-3 relative (max |dS| / max |S|).  Tighter bounds guard each kernel's expected accuracy.
+Cases: float64 fixtures; BASELINE config 4 (T=4096, Hq=16, Hv=32, C=64) in full; the
+reference driver's LCG inputs and shape (Hv=48, T=512); ragged T and head maps with
+Hv % Hq != 0; batches; state continuity across calls (prefill -> prefill -> decode); BASELINE
+config 5 (16 sequences x 32 heads, N(0, 0.02) state) over 64 steps in full and 512 steps on a
+subset of sequences.
+"""
+import numpy as np
+import pytest
+
+import tsa
+
+pytestmark = pytest.mark.gpu
+D = 128
+OUT_GATE, STATE_GATE = 2e-2, 1e-3
+
+
+def _inputs(rng, B, T, Hq, Hv, sstd=0.0):
+    l2n = lambda x: x / np.linalg.norm(x, axis=-1, keepdims=True)
+    q = l2n(rng.standard_normal((B, T, Hq, D))).astype(np.float16)
+    k = l2n(rng.standard_normal((B, T, Hq, D))).astype(np.float16)
+    v = rng.standard_normal((B, T, Hv, D)).astype(np.float16)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((B, T, Hv))))).astype(np.float32)
+    g = (-np.logaddexp(0.0, rng.standard_normal((B, T, Hv)))).astype(np.float32)
+    st = (sstd * rng.standard_normal((B, Hv, D, D))).astype(np.float32)
+    return q, k, v, g, beta, st
+
+
+def _dev(dev, *arrays):
+    import torch
+    return [torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in arrays]
+
+
+def _gpu(dev, kind, q, k, v, g, beta, st):
+    import torch
+    tq, tk, tv, tg, tb, ts = _dev(dev, q, k, v, g, beta, st)
+    if kind == "chunked":
+        o = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts)
+    elif kind == "recurrent":
+        o = tsa.gdn_recurrent_fwd(tq, tk, tv, tg, tb, ts)
+    else:
+        o = tsa.gdn_naive(tq, tk, tv, tg, tb, ts)
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), ts.cpu().numpy()
+
+
+def _rel(a, ref):
+    return float(np.abs(a - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def _check(o, s, o_ref, s_ref, out_tol, state_tol, label=""):
+    eo, es = float(np.abs(o - o_ref).max()), _rel(s, s_ref)
+    print(f"{label} out max-abs {eo:.2e}  state rel {es:.2e}")
+    assert eo < min(out_tol, OUT_GATE) and es < min(state_tol, STATE_GATE)
+
+
+# per-kernel expected accuracy: chunked uses fp16 MFMA operands, the others fp32 FMA
+TOL = {"chunked": (2e-3, 8e-4), "recurrent": (2e-3, 1e-5), "naive": (2e-3, 1e-5)}
+
+
+@pytest.mark.parametrize("kind", ["chunked", "recurrent", "naive"])
+@pytest.mark.parametrize("i", range(3))
+def test_golden_fixtures(dev, golden, kind, i):
+    g = golden("gdn_golden.npz")
+    q, k, v, gl, beta, s0 = (g[f"c{i}_{n}"] for n in ("q", "k", "v", "g", "beta", "state0"))
+    o, s = _gpu(dev, kind, q, k, v, gl, beta, s0.astype(np.float32))
+    _check(o, s, g[f"c{i}_out"], g[f"c{i}_state1"], *TOL[kind], label=f"{kind} golden{i}")
+
+
+@pytest.mark.parametrize("kind", ["chunked", "recurrent"])
+def test_config4_full(dev, orc, kind):
+    rng = np.random.default_rng(401)
+    q, k, v, g, beta, st = _inputs(rng, 1, 4096, 16, 32)
+    o, s = _gpu(dev, kind, q, k, v, g, beta, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    _check(o, s, o_ref, s_ref, *TOL[kind], label=f"{kind} config4")
+
+
+@pytest.mark.parametrize("kind", ["chunked", "recurrent"])
+def test_reference_lcg_shape(dev, orc, kind):
+    q, k, v, g, b = orc.gdn_lcg_inputs(512, 16, 48)
+    h = lambda a: a.astype(np.float16)[None]
+    q, k, v, g, b = h(q), h(k), h(v), g[None], b[None]
+    st = np.zeros((1, 48, D, D), np.float32)
+    o, s = _gpu(dev, kind, q, k, v, g, b, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, b, st)
+    _check(o, s, o_ref, s_ref, *TOL[kind], label=f"{kind} lcg T=512 Hv=48")
+
+
+@pytest.mark.parametrize("kind", ["chunked", "recurrent"])
+@pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 100, 129])
+def test_ragged_and_head_map(dev, orc, kind, T):
+    rng = np.random.default_rng(T + (kind == "chunked") * 1000)
+    q, k, v, g, beta, st = _inputs(rng, 2, T, 3, 4, sstd=0.02)  # Hv % Hq != 0
+    o, s = _gpu(dev, kind, q, k, v, g, beta, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    _check(o, s, o_ref, s_ref, *TOL[kind], label=f"{kind} T={T}")
+
+
+def test_state_continuity_prefill_prefill_decode(dev, orc):
+    import torch
+    rng = np.random.default_rng(402)
+    T1, T2 = 100, 60
+    q, k, v, g, beta, st = _inputs(rng, 2, T1 + T2 + 1, 2, 4, sstd=0.02)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    ts = _dev(dev, st)[0]
+    outs = []
+    for a, b in ((0, T1), (T1, T1 + T2)):
+        tq, tk, tv, tg, tb = _dev(dev, q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b], beta[:, a:b])
+        outs.append(tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts).float().cpu().numpy())
+    t = T1 + T2
+    tq, tk, tv, tg, tb = _dev(dev, q[:, t], k[:, t], v[:, t], g[:, t], beta[:, t])
+    od = tsa.gdn_decode_step(tq, tk, tv, tg, tb, ts)
+    torch.cuda.synchronize()
+    o = np.concatenate(outs + [od.float().cpu().numpy()[:, None]], axis=1)
+    _check(o, ts.cpu().numpy(), o_ref, s_ref, 2e-3, 8e-4, label="continuity")
+
+
+def _decode_run(dev, q, k, v, g, beta, st):
+    """Run T single-token steps (inputs [B,T,...]); returns outputs [B,T,Hv,D] and state."""
+    import torch
+    B, T = q.shape[:2]
+    ts = _dev(dev, st)[0]
+    # step-major copies so each step's inputs are contiguous [B, H, D]
+    sw = lambda a: np.ascontiguousarray(np.swapaxes(a, 0, 1))
+    tq, tk, tv, tg, tb = _dev(dev, sw(q), sw(k), sw(v), sw(g), sw(beta))
+    outs = [tsa.gdn_decode_step(tq[t], tk[t], tv[t], tg[t], tb[t], ts) for t in range(T)]
+    torch.cuda.synchronize()
+    o = torch.stack(outs, dim=1).float().cpu().numpy()
+    return o, ts.cpu().numpy()
+
+
+def test_config5_decode_64_steps_full(dev, orc):
+    rng = np.random.default_rng(501)
+    q, k, v, g, beta, st = _inputs(rng, 16, 64, 16, 32, sstd=0.02)
+    o, s = _decode_run(dev, q, k, v, g, beta, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    _check(o, s, o_ref, s_ref, 2e-3, 1e-5, label="decode 16x32 heads, 64 steps")
+
+
+def test_config5_decode_512_steps_subset(dev, orc):
+    rng = np.random.default_rng(502)
+    q, k, v, g, beta, st = _inputs(rng, 16, 512, 16, 32, sstd=0.02)
+    o, s = _decode_run(dev, q, k, v, g, beta, st)
+    sub = [0, 7, 15]
+    o_ref, s_ref = orc.gdn_serial(q[sub], k[sub], v[sub], g[sub], beta[sub], st[sub])
+    _check(o[sub], s[sub], o_ref, s_ref, 2e-3, 1e-5, label="decode 512 steps (3 seqs checked)")
+
+
+def test_recurrent_equals_decode_steps(dev):
+    rng = np.random.default_rng(503)
+    q, k, v, g, beta, st = _inputs(rng, 3, 9, 2, 4, sstd=0.02)
+    o_r, s_r = _gpu(dev, "recurrent", q, k, v, g, beta, st)
+    o_d, s_d = _decode_run(dev, q, k, v, g, beta, st)
+    # same kernel code path and arithmetic order: bit-identical
+    assert np.array_equal(o_r, o_d) and np.array_equal(s_r, s_d)
+
+
+def test_workspace_too_small_raises(dev):
+    import torch
+    rng = np.random.default_rng(504)
+    q, k, v, g, beta, st = _dev(dev, *_inputs(rng, 1, 70, 1, 2))
+    need = tsa.gdn_chunked_workspace_bytes(1, 70, 1, 2)
+    ws = torch.empty(need - 256, dtype=torch.uint8, device=dev)
+    with pytest.raises(tsa.TsaError) as e:
+        tsa.gdn_chunked_fwd(q, k, v, g, beta, st, ws=ws)
+    assert e.value.code == tsa.TSA_ERR_WORKSPACE

@@ -1,0 +1,60 @@
+"""Oracle: fp16 conversion and the reference's input generators.
+
+Pins: f2h / h2f against numpy's IEEE binary16 (round to nearest even) over every fp16 bit
+pattern and over edge values (ties, subnormals, overflow, NaN); the GDN LCG against values
+computed with Python integers (tests/golden/lcg_golden.npz); the mt19937 normal generator
+by its moments and determinism (its exact stream is libstdc++'s, as in the reference).
+"""
+import numpy as np
+
+
+def test_h2f_all_bit_patterns(orc):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ours = orc.h2f(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f2h_matches_numpy_rne(orc):
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * 10 ** rng.uniform(-9, 5, 200000).astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 65536.0, 1e30, -1e30, np.inf, -np.inf,
+                  2 ** -24, 2 ** -25, 3 * 2 ** -26, 2 ** -25 * 1.0000001, 2 ** -14, 2 ** -14 * (1 - 2 ** -11),
+                  1 + 2 ** -11, 1 + 3 * 2 ** -11, 1 + 2 ** -11 + 2 ** -20], np.float32),
+        # every fp16 value and the midpoints between neighbours (ties to even)
+        np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32),
+    ])
+    mids = (np.arange(0, 0x7BFF, dtype=np.uint16).view(np.float16).astype(np.float64)
+            + np.arange(1, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float64)) / 2
+    x = np.concatenate([x, mids.astype(np.float32), -mids.astype(np.float32)])
+    ours = orc.f2h(x)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ours, ref), np.flatnonzero(ours != ref)[:10]
+    assert np.isnan(orc.h2f(orc.f2h(np.array([np.nan], np.float32))))[0]
+
+
+def test_lcg_known_answers(orc, golden):
+    g = golden("lcg_golden.npz")
+    q, k, v, gl, b = orc.gdn_lcg_inputs(1, 16, 48, 128)
+    assert np.array_equal(q.reshape(-1)[:8], g["q_first"])
+    assert np.array_equal(k.reshape(-1)[:8], g["k_first"])
+    # ranges stated by the generator (src/gdn_sm75.cu:1275-1278)
+    assert np.abs(v).max() <= 0.1 and gl.min() >= -0.225 and gl.max() <= -0.175
+    assert b.min() >= 0.4 and b.max() <= 0.8
+
+
+def test_mt_normal_half_moments_and_determinism(orc):
+    a = orc.mt_normal_half(42, 0.0, 0.5, 1 << 16, 3)
+    b = orc.mt_normal_half(42, 0.0, 0.5, 1 << 16, 3)
+    assert np.array_equal(a, b)
+    x = a.view(np.float16).astype(np.float64)
+    for t in range(3):
+        assert abs(x[t].mean()) < 0.01 and abs(x[t].std() - 0.5) < 0.01
+    # the three tensors continue one stream, so they differ
+    assert not np.array_equal(a[0], a[1])
+    c = orc.mt_normal_half(43, 0.0, 0.5, 1 << 16, 1)
+    assert not np.array_equal(a[0], c[0])

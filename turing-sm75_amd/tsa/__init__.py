@@ -39,10 +39,10 @@ _SIGNATURES = {
     "tsa_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp]),
     "tsa_attn_naive": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp]),
     "tsa_gdn_chunked_workspace_bytes": (_sz, [_i] * 7),
-    "tsa_gdn_chunked_fwd": (_i, [_vp] * 7 + [_i] * 8 + [_f, _vp, _sz, _vp]),
-    "tsa_gdn_recurrent_fwd": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp]),
+    "tsa_gdn_chunked_fwd": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp, _sz, _vp]),
+    "tsa_gdn_recurrent_fwd": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
     "tsa_gdn_decode_step": (_i, [_vp] * 7 + [_i] * 5 + [_f, _vp]),
-    "tsa_gdn_naive": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp]),
+    "tsa_gdn_naive": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
 }
 
 
