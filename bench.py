@@ -126,9 +126,9 @@ def cpu_baselines(torch, a, pre, dec, threads):
     import numpy as np
     import oracle
     res = {}
-    # attention: every row of 2 of the 32 heads (causal), all host threads
+    # attention: every row of 8 of the 32 heads (causal), all host threads
     s = ATTN
-    nh = 2
+    nh = 8
     q, k, v = (a[n][:, :nh].cpu().numpy() for n in ("q", "k", "v"))
     rows = np.arange(nh * s["S"], dtype=np.int64)
     t0 = time.perf_counter()
@@ -137,11 +137,11 @@ def cpu_baselines(torch, a, pre, dec, threads):
     fl = attn_flops(1, nh, s["S"], s["D"], True)
     res["attn_fwd"] = {"value": fl / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
                        "sample": f"all {s['S']} causal rows of {nh} of {s['H']} heads ({dt:.1f} s)"}
-    # prefill: serial recurrence, all 4096 tokens of 8 of the 32 V-heads
+    # prefill: serial recurrence, all 4096 tokens of all 32 V-heads
     p = PREFILL
-    hv_s = 8
+    hv_s = 32
     g = lambda n: pre[n].float().cpu().numpy()
-    qn, kn = g("q")[:, :, :hv_s], g("k")[:, :, :hv_s]  # V-heads 0..7 read QK heads 0..7
+    qn, kn = g("q"), g("k")
     vn, bn, gn = g("v")[:, :, :hv_s], g("beta")[:, :, :hv_s], g("g")[:, :, :hv_s]
     st = np.zeros((1, hv_s, p["d"], p["d"]), np.float32)
     t0 = time.perf_counter()
@@ -150,9 +150,9 @@ def cpu_baselines(torch, a, pre, dec, threads):
     tok_s = p["B"] * p["T"] / (dt * p["Hv"] / hv_s)
     res["gdn_prefill"] = {"value": tok_s, "unit": "tok/s", "cores": threads, "kind": "port",
                           "sample": f"T={p['T']} for {hv_s} of {p['Hv']} V-heads ({dt:.1f} s), scaled to all heads"}
-    # decode: 64 single-token steps over the full 16 x 32-head state
+    # decode: 256 single-token steps over the full 16 x 32-head state
     d = DECODE
-    steps = 64
+    steps = 256
     qd, kd, vd = (dec[n].float().cpu().numpy()[:, None] for n in ("q", "k", "v"))
     bd, gd = (dec[n].cpu().numpy()[:, None] for n in ("beta", "g"))
     st = dec["states"][0].cpu().numpy()
@@ -173,6 +173,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--decode-steps", type=int, default=512,
                     help="length of the extra decode-only run (the 512-step workload)")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="after the measurements, run one plain device copy of this many MiB "
+                         "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the hot path's sharding (heads / sequences) is "
@@ -258,6 +261,15 @@ def main():
     torch.cuda.synchronize()
     dec_rot_ms = e0.elapsed_time(e1) / n
     dec_res_ms = e2.elapsed_time(e3) / n
+
+    if args.copy_calibration_mib > 0:
+        n_el = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.ones(n_el, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     finite = bool(torch.isfinite(a["o"]).all() and torch.isfinite(pre["out"]).all()
                   and torch.isfinite(pre["state"]).all() and torch.isfinite(dec["out"]).all())
