@@ -53,4 +53,14 @@ __device__ __forceinline__ float sum8(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
+// outstanding global load and store of the wave (vmcnt counts both), which would drain
+// prefetches issued for later iterations; use this one where no global memory written
+// by one wave is read by another wave of the workgroup.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace tsa
