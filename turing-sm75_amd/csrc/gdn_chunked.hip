@@ -341,7 +341,6 @@ struct CarryLds {
     OutSlot os[2];
     uint4 XS[2][kStrips][6][64];     // chain -> output: S operands (4) and Vnew operands (2)
     half_t OS[2][32 * 32];           // per output wave: its 32 tokens x 32 columns of O
-    unsigned PF[64];                 // landing words of the L2 prefetch (never read)
 };
 
 // 16-B chunk swizzle of the [64][64] Aqk tile: 16 consecutive rows at one chunk are
@@ -352,105 +351,112 @@ __device__ __forceinline__ int aqk_off(int r, int c) {
 
 typedef __attribute__((address_space(3))) void* lds_void_t;
 
-// One LDS-DMA instruction: lane l copies 16 bytes from src into LDS dst_base + 16*l
-// (M0 holds the wave's LDS base).  Written as inline asm on purpose: the compiler does not
-// track LDS written by DMA slot by slot and would wait for every DMA in flight before the
-// first LDS read of the other slot; the kernel orders DMA and reads itself with
-// dma_barrier(), the only consumer-side wait these writes need.
-__device__ __forceinline__ void dma16(const void* src, const void* dst_base) {
-    const unsigned m0v = __builtin_amdgcn_readfirstlane(
-        (unsigned)(uintptr_t)(lds_void_t)const_cast<void*>(dst_base));
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(src), "{m0}"(m0v) : "memory");
+// Per-chunk copies into LDS: 62 one-KiB LDS-DMA instructions (global_load_lds_dwordx4,
+// lane l copies 16 bytes to M0 + 16*l).  Instruction n < 37 fills the chain slot at byte
+// 1024*n (K tile n < 16, W tile, U strips 32..35, E/Dg 36); n >= 37 fills the out slot at
+// byte 1024*(n-37) (Q tile, Aqk tile, E/Dg 61).  The structs' members are laid out in that
+// order so that the LDS offset is just 1024 * tile index.  The four DMA waves (4-7) take
+// n = w + 4j; each lane's source offset for its instructions is fixed for the whole loop
+// and computed once, so an instruction costs a scalar M0 write and the DMA itself.
+constexpr int kDmaN = 62, kDmaChain = 37, kDmaPerWave = 16;
+constexpr int kDmaEChain = 36, kDmaEOut = 61;  // 512-byte copies: lanes 0-31 only
+
+// Source byte offset of instruction n for this lane, from the instruction's base pointer:
+// the row base of the chunk's first token (K / Q tiles, rows at rowbytes apart, rows
+// past `lastrow` clamped to it: they only meet zero coefficients) or the chunk's workspace.
+__device__ __forceinline__ unsigned dma_src_off(int n, int lane, unsigned rowbytes, int pair, int lastrow) {
+    const int i = n < kDmaChain ? n : n - kDmaChain;
+    const bool chainslot = n < kDmaChain;
+    if (i < 16) {                                    // K or Q rows, swizzled 16-B chunks
+        const int P = i * 64 + lane, row = P >> 4, cch = (P & 15) ^ swz(row);
+        return (unsigned)min(row, lastrow) * rowbytes + cch * 16;
+    }
+    if (chainslot) {
+        if (i < 32) {                                // W rows, swizzled
+            const int P = (i - 16) * 64 + lane, row = P >> 4, cch = (P & 15) ^ swz(row);
+            return kWsW + (row * kD + cch * 8) * 2;
+        }
+        if (i < 36) return kWsU + pair * 4096 + (i - 32) * 1024 + lane * 16;  // own U strips
+        return kWsG + (lane & 31) * 16;
+    }
+    if (i < 24) {                                    // Aqk rows, 8-chunk swizzle
+        const int P = (i - 16) * 64 + lane, row = P >> 3, cch = (P & 7) ^ ((row >> 1) & 7);
+        return kWsAqk + (row * kC + cch * 8) * 2;
+    }
+    return kWsG + (lane & 31) * 16;
 }
 
-// DMA of the chain operands of one chunk into a chain slot (37 one-KiB instructions) and
-// of the output operands of one chunk into an out slot (25 instructions), spread over the
-// four DMA waves (4-7).  A wave stalls at issue once its requests to far memory pile up,
-// so the copies are issued by waves that do nothing else.  Rows past T are clamped to the
-// last valid row: they only meet zero coefficients (U, W and beta are zero there).
-__device__ __forceinline__ void dma_chain(ChainSlot& cs, const half_t* k, const unsigned char* wsc,
-                                          int b, int T, int Hq, int hq, int t0, int pair) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int i = wave - 4; i < 37; i += 4) {
-        if (i < 16) {                       // K tile, 1 KiB block i
-            const int P = i * 64 + lane, row = P >> 4, cch = (P & 15) ^ swz(row);
-            const int tt = min(t0 + row, T - 1);
-            dma16(k + (((size_t)b * T + tt) * Hq + hq) * kD + cch * 8, cs.K + i * 512);
-        } else if (i < 32) {                // W tile
-            const int bi = i - 16, P = bi * 64 + lane, row = P >> 4, cch = (P & 15) ^ swz(row);
-            dma16(wsc + kWsW + (size_t)(row * kD + cch * 8) * 2, cs.W + bi * 512);
-        } else if (i < 36) {                // U strips 2*pair, 2*pair+1: 4 KiB linear
-            const int bi = i - 32;
-            dma16(wsc + kWsU + (size_t)pair * 4096 + (size_t)bi * 1024 + lane * 16, cs.U + bi * 512);
-        } else if (lane < 32) {             // E, Dg: 512 B
-            dma16(wsc + kWsG + lane * 16, cs.E);
-        }
-    }
-}
-__device__ __forceinline__ void dma_out(OutSlot& os, const half_t* q, const unsigned char* wsc,
-                                        int b, int T, int Hq, int hq, int t0) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int i = (wave - 3) & 3; i < 25; i += 4) {  // 62 instructions in all: 15 or 16 per wave
-        if (i < 16) {                       // Q tile
-            const int P = i * 64 + lane, row = P >> 4, cch = (P & 15) ^ swz(row);
-            const int tt = min(t0 + row, T - 1);
-            dma16(q + (((size_t)b * T + tt) * Hq + hq) * kD + cch * 8, os.Q + i * 512);
-        } else if (i < 24) {                // Aqk tile
-            const int bi = i - 16, P = bi * 64 + lane, row = P >> 3, cch = (P & 7) ^ ((row >> 1) & 7);
-            dma16(wsc + kWsAqk + (size_t)(row * kC + cch * 8) * 2, os.A + bi * 512);
-        } else if (lane < 32) {
-            dma16(wsc + kWsG + lane * 16, os.E);
-        }
-    }
+// Issue instruction n: src = base + off (saddr form: 64-bit base in SGPRs, 32-bit VGPR
+// offset).  Written as inline asm on purpose: the compiler does not track LDS written by
+// DMA slot by slot and would wait for every DMA in flight before the first LDS read of the
+// other slot; the kernel orders the copies and the reads itself (dma_wait_barrier).
+__device__ __forceinline__ void dma_issue(const void* base, unsigned off, unsigned lds_addr, bool half) {
+    if (!half || (threadIdx.x & 63) < 32)
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(off), "s"(base), "{m0}"(lds_addr)
+                     : "memory");
 }
 
-// L2 prefetch of one chunk: one 4-byte LDS-DMA per 128-byte line, landing in PF.  Lines
-// shared by the four column workgroups of a head (K, Q, W, Aqk, E/Dg: 452 lines) are split
-// four ways, each workgroup adds its own U strips (32 lines): 3 instructions, every lane
-// active (spare lanes repeat the first E line).  Then the DMA of the chunk's tiles hits L2.
-constexpr int kPfShared = 452 / 4;
-constexpr int kPfInstr = 3;
-__device__ __forceinline__ void prefetch_l2(const half_t* q, const half_t* k, const unsigned char* wsc,
-                                            int b, int T, int Hq, int hq, int t0, int pair,
-                                            const unsigned* pf) {
-    const int lane = threadIdx.x & 63;
-    const unsigned m0v = (unsigned)(uintptr_t)(lds_void_t)const_cast<unsigned*>(pf);
-#pragma unroll
-    for (int j = 0; j < kPfInstr; ++j) {
-        const int slot = 64 * j + lane;
-        const unsigned char* p = wsc + kWsG;
-        if (slot < kPfShared) {
-            const int L = pair + 4 * slot;  // < 452
-            if (L < 256) {
-                const int tt = min(t0 + ((L & 127) >> 1), T - 1);
-                const half_t* base = L < 128 ? k : q;
-                p = reinterpret_cast<const unsigned char*>(base + (((size_t)b * T + tt) * Hq + hq) * kD) + 128 * (L & 1);
-            } else if (L < 384) {
-                p = wsc + kWsW + (L - 256) * 128;
-            } else if (L < 448) {
-                p = wsc + kWsAqk + (L - 384) * 128;
-            } else {
-                p = wsc + kWsG + (L - 448) * 128;
-            }
-        } else if (slot < kPfShared + 32) {
-            p = wsc + kWsU + pair * 4096 + (slot - kPfShared) * 128;
-        }
-        asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" :: "v"(p), "{m0}"(m0v) : "memory");
-    }
-}
-
-// Wait for this wave's DMA, then a barrier over LDS: after it every wave sees every wave's
-// DMA data.  The prefetching wave issued its kPfInstr prefetches last and vector loads
-// complete in issue order, so vmcnt(kPfInstr) covers its DMA and leaves the prefetches in
-// flight (vmcnt also counts stores; their completion is not needed here).
-template <bool kPrefetcher>
-__device__ __forceinline__ void dma_barrier() {
-    if (kPrefetcher)
-        __builtin_amdgcn_s_waitcnt(0x0F70 | kPfInstr);  // vmcnt(3)
-    else
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt left at their maxima
+// Wait for this wave's copies (vmcnt counts them), then a barrier over LDS: after it every
+// wave sees every wave's copies.
+__device__ __forceinline__ void dma_wait_barrier() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt left at their maxima
     lds_barrier();
 }
+
+// The loop of DMA wave W (0..3): instruction n = W + 4j is a constant in each unrolled
+// step, so its kind, base pointer and LDS address fold.  Iteration it copies the chain
+// operands of chunk it+1 into cs[(it+1)&1] and the output operands of chunk it into
+// os[it&1] (the prologue: chunk 0 into cs[0]), then waits for them and meets the barrier.
+// A chunk that ends past T recomputes its K / Q offsets with clamped rows.
+template <int W>
+__device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const unsigned char* kh,
+                                         const unsigned char* qh, const unsigned char* wsh,
+                                         unsigned rowbytes, int pair, int T, int nch) {
+    constexpr int kJ = (kDmaN - W + 3) / 4;
+    const int lane = threadIdx.x & 63;
+    unsigned off[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) off[j] = dma_src_off(W + 4 * j, lane, rowbytes, pair, kC - 1);
+    // slot_lds: cs[0], cs[1], os[0], os[1]
+    auto copies = [&](int pc, int po, int cn, int co) {
+        const bool do_c = cn < nch, do_o = co >= 0 && co < nch;
+        const int last_c = min(kC - 1, T - 1 - cn * kC), last_o = min(kC - 1, T - 1 - co * kC);
+        const unsigned char* kb = kh + (size_t)cn * kC * rowbytes;
+        const unsigned char* wc = wsh + (size_t)cn * kWsChunk;
+        const unsigned char* qb = qh + (size_t)co * kC * rowbytes;
+        const unsigned char* wo = wsh + (size_t)co * kWsChunk;
+        auto issue_all = [&](auto Ragged) {
+#pragma unroll
+            for (int j = 0; j < kJ; ++j) {
+                const int n = W + 4 * j;
+                const bool chainslot = n < kDmaChain;
+                const int i = chainslot ? n : n - kDmaChain;
+                const bool rows = i < 16;
+                if (chainslot ? !do_c : !do_o) continue;
+                unsigned o = off[j];
+                if (decltype(Ragged)::value && rows)
+                    o = dma_src_off(n, lane, rowbytes, pair, chainslot ? last_c : last_o);
+                const unsigned char* base = chainslot ? (rows ? kb : wc) : (rows ? qb : wo);
+                const unsigned lds = (chainslot ? slot_lds[pc] : slot_lds[2 + po]) + 1024u * i;
+                dma_issue(base, o, lds, n == kDmaEChain || n == kDmaEOut);
+            }
+        };
+        if ((do_c && last_c < kC - 1) || (do_o && last_o < kC - 1))
+            issue_all(std::true_type{});
+        else
+            issue_all(std::false_type{});
+    };
+    copies(0, 0, 0, -1);
+    dma_wait_barrier();
+    for (int it = 0; it <= nch; it += 2) {
+        copies(1, 0, it + 1, it);
+        dma_wait_barrier();
+        if (it + 1 > nch) break;
+        copies(0, 1, it + 2, it + 1);
+        dma_wait_barrier();
+    }
+}
+
 
 // Chain step for one chunk: strip S (fp32 accumulators) <- next state, and the S / Vnew
 // operands handed to the output waves in XS.
@@ -595,7 +601,8 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
                 const unsigned char* __restrict__ ws, float* __restrict__ state,
                 half_t* __restrict__ out, int T, int Hq, int Hv, int nch, int BHv, float scale) {
     __shared__ CarryLds sm;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: role branches are scalar
     const int g = lane >> 4, c = lane & 15;
     // block id = pair * BHv + bh: all column pairs of one head share an XCD when BHv % 8 == 0
     const int pair = blockIdx.x / BHv;
@@ -608,9 +615,8 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
     // Pipeline, iteration it.  Chain waves: process chunk it from cs[it&1].  Output waves:
     // store the O tile of chunk it-2 staged in LDS, then compute the output of chunk it-1
     // from os[(it-1)&1] and XS[(it-1)&1].  DMA waves: copy the chain operands of chunk it+1
-    // into cs[(it+1)&1] and the output operands of chunk it into os[it&1]; wave 7 then
-    // prefetches chunk it+3 into L2; wait for the copies.  Then the workgroup meets at a
-    // barrier.
+    // into cs[(it+1)&1] and the output operands of chunk it into os[it&1], then wait for
+    // the copies.  Then the workgroup meets at a barrier.
     float4_t S[8];
     float* Sg = state + ((size_t)bh * kD + (pair * kStrips + sl) * 16 + c) * kD;
     if (chain) {
@@ -620,16 +626,7 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
             S[m] = float4_t{v4.x, v4.y, v4.z, v4.w};
         }
     }
-    if (dmaw) {
-        dma_chain(sm.cs[0], k, wsh, b, T, Hq, hq, 0, pair);
-        if (wave == 7)
-            for (int cp = 1; cp <= 2; ++cp) {
-                const int cc = min(cp, nch - 1);
-                prefetch_l2(q, k, wsh + (size_t)cc * kWsChunk, b, T, Hq, hq, cc * kC, pair, sm.PF);
-            }
-    }
-    dma_barrier<false>();
-
+    if (!dmaw) dma_wait_barrier();  // matches the DMA waves' prologue barrier
     // Each role runs its own loop (one barrier per iteration in each), so no role's loop
     // state occupies registers in another role's code.  `it` runs 0..nch; the loop is
     // unrolled by two so slot indices are constants.
@@ -653,23 +650,18 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
             lds_barrier();
         }
     } else {
-        auto dma_step = [&](auto P, int it) {
-            constexpr int p = decltype(P)::value;
-            if (it + 1 < nch)
-                dma_chain(sm.cs[p ^ 1], k, wsh + (size_t)(it + 1) * kWsChunk, b, T, Hq, hq, (it + 1) * kC, pair);
-            if (it < nch) dma_out(sm.os[p], q, wsh + (size_t)it * kWsChunk, b, T, Hq, hq, it * kC);
-            if (wave == 7) {
-                const int cc = min(it + 3, nch - 1);
-                prefetch_l2(q, k, wsh + (size_t)cc * kWsChunk, b, T, Hq, hq, cc * kC, pair, sm.PF);
-                dma_barrier<true>();
-            } else {
-                dma_barrier<false>();
-            }
-        };
-        for (int it = 0; it <= nch; it += 2) {
-            dma_step(std::integral_constant<int, 0>{}, it);
-            if (it + 1 > nch) break;
-            dma_step(std::integral_constant<int, 1>{}, it + 1);
+        const unsigned rowbytes = (unsigned)Hq * kD * 2;
+        const unsigned char* kh = reinterpret_cast<const unsigned char*>(k + ((size_t)b * T * Hq + hq) * kD);
+        const unsigned char* qh = reinterpret_cast<const unsigned char*>(q + ((size_t)b * T * Hq + hq) * kD);
+        const unsigned slot_lds[4] = {(unsigned)(uintptr_t)(lds_void_t)(void*)&sm.cs[0],
+                                      (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.cs[1],
+                                      (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.os[0],
+                                      (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.os[1]};
+        switch (wave) {
+            case 4: dma_role<0>(slot_lds, kh, qh, wsh, rowbytes, pair, T, nch); break;
+            case 5: dma_role<1>(slot_lds, kh, qh, wsh, rowbytes, pair, T, nch); break;
+            case 6: dma_role<2>(slot_lds, kh, qh, wsh, rowbytes, pair, T, nch); break;
+            default: dma_role<3>(slot_lds, kh, qh, wsh, rowbytes, pair, T, nch); break;
         }
     }
     if (chain) {
