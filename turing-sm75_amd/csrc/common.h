@@ -25,6 +25,12 @@ __device__ __forceinline__ float4_t mfma16(const half8_t& a, const half8_t& b, c
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// D(16x16 fp32) += A(16x4 fp32) * B(4x16 fp32).  Lane l holds A[l%16][l/16], B[l/16][l%16],
+// and D[4*(l/16) + r][l%16] in register r.
+__device__ __forceinline__ float4_t mfma16f32(float a, float b, const float4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 // Transposing LDS read (ds_read_b64_tr_b16).  Within each group of 16 lanes, source lane
 // s supplies the address of 4 consecutive fp16 values; result lane i, slot j receives
 // element i%4 of source lane 4*j + i/4.

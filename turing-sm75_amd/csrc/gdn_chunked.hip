@@ -215,38 +215,27 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
         for (int t = 0; t < 16; ++t) sm.Tm[16 * bi + t][16 * bi + cj] = x[t];
     }
     lds_barrier();
-    if (wave < 3) {  // block column j = wave: T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj, i > j
-        const int j = wave, rr = lane >> 4, cc = lane & 15;
+    if (wave < 3) {  // block column j = wave: T_ij = -T_ii X, X = sum_{k=j}^{i-1} A_ik T_kj, i > j
+        // 16x16x16 fp32 block products on v_mfma_f32_16x16x4_f32 (lane l: A[l%16][l/16],
+        // B[l/16][l%16], D[4*(l/16) + r][l%16]); the diagonal blocks hold zeros above the
+        // diagonal, so no masking is needed.
+        const int j = wave, r16 = lane & 15, k4 = lane >> 4;
         for (int i = j + 1; i < 4; ++i) {
-            float x[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int kb = j; kb < i; ++kb) {
+            float4_t x = {};
+            for (int kb = j; kb < i; ++kb)
 #pragma unroll
-                for (int m4 = 0; m4 < 4; ++m4) {
-                    float tv[4];
+                for (int s4 = 0; s4 < 4; ++s4)
+                    x = mfma16f32(sm.A[16 * i + r16][16 * kb + 4 * s4 + k4],
+                                  sm.Tm[16 * kb + 4 * s4 + k4][16 * j + r16], x);
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) tv[u] = sm.Tm[16 * kb + 4 * m4 + u][16 * j + cc];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float4 a4 = *reinterpret_cast<const float4*>(&sm.A[16 * i + 4 * rr + e][16 * kb + 4 * m4]);
-                        x[e] = fmaf(a4.x, tv[0], x[e]);
-                        x[e] = fmaf(a4.y, tv[1], x[e]);
-                        x[e] = fmaf(a4.z, tv[2], x[e]);
-                        x[e] = fmaf(a4.w, tv[3], x[e]);
-                    }
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sm.X[j][4 * rr + e][cc] = x[e];
+            for (int r = 0; r < 4; ++r) sm.X[j][4 * k4 + r][r16] = x[r];
             wave_lds_sync();
+            float4_t t = {};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = 4 * rr + e;
-                float acc = 0.f;
+            for (int s4 = 0; s4 < 4; ++s4)
+                t = mfma16f32(sm.Tm[16 * i + r16][16 * i + 4 * s4 + k4], sm.X[j][4 * s4 + k4][r16], t);
 #pragma unroll
-                for (int m = 0; m < 16; ++m)
-                    if (m <= r) acc = fmaf(sm.Tm[16 * i + r][16 * i + m], sm.X[j][m][cc], acc);
-                sm.Tm[16 * i + r][16 * j + cc] = -acc;
-            }
+            for (int r = 0; r < 4; ++r) sm.Tm[16 * i + 4 * k4 + r][16 * j + r16] = -t[r];
             wave_lds_sync();
         }
     }
