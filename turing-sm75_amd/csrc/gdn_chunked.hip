@@ -94,18 +94,17 @@ struct PrepLds {
         half_t V[kC * kD];
         half_t Wst[kC * kD];
     };
-    union {             // Tm; U staging at the end
+    union {             // Aqk staging first; then Tm; U staging at the end
+        half_t Aqk[kC * kC];
         float Tm[kC][kA];
         half_t Ust[kC * kD];
     };
-    half_t Aqk[kC * kC];  // Aqk staging
-    float X[3][16][17];   // per-wave scratch of the off-diagonal solve
     float G[kC];
     float bt[kC];
     float bg[kC];
 };
 
-__global__ void __launch_bounds__(kThreads, 2)
+__global__ void __launch_bounds__(kThreads, 3)
 gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
                const half_t* __restrict__ v, const float* __restrict__ g_log,
                const float* __restrict__ beta, unsigned char* __restrict__ ws, int T, int Hq,
@@ -193,13 +192,14 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
     }
     lds_barrier();
 
-    // ---- 3. Aqk out; Tm = (I + A)^-1 ----
+    // ---- 3. Aqk out (its staging shares LDS with Tm); Tm = (I + A)^-1 ----
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int id = it * kThreads + tid;
         *reinterpret_cast<uint4*>(wsc + kWsAqk + (size_t)id * 16) =
             *reinterpret_cast<const uint4*>(sm.Aqk + id * 8);
     }
+    lds_barrier();
     if (wave == 0) {  // the four 16x16 diagonal blocks, one column per lane
         const int bi = lane >> 4, cj = lane & 15;
         float x[16];
@@ -218,7 +218,9 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
     if (wave < 3) {  // block column j = wave: T_ij = -T_ii X, X = sum_{k=j}^{i-1} A_ik T_kj, i > j
         // 16x16x16 fp32 block products on v_mfma_f32_16x16x4_f32 (lane l: A[l%16][l/16],
         // B[l/16][l%16], D[4*(l/16) + r][l%16]); the diagonal blocks hold zeros above the
-        // diagonal, so no masking is needed.
+        // diagonal, so no masking is needed.  X stays in registers: register s of lane l
+        // holds X[4*(l/16) + s][l%16], which is the B operand of k-step s when the A operand
+        // supplies column 4*(l/16) + s of T_ii.
         const int j = wave, r16 = lane & 15, k4 = lane >> 4;
         for (int i = j + 1; i < 4; ++i) {
             float4_t x = {};
@@ -227,13 +229,10 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
                 for (int s4 = 0; s4 < 4; ++s4)
                     x = mfma16f32(sm.A[16 * i + r16][16 * kb + 4 * s4 + k4],
                                   sm.Tm[16 * kb + 4 * s4 + k4][16 * j + r16], x);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sm.X[j][4 * k4 + r][r16] = x[r];
-            wave_lds_sync();
             float4_t t = {};
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4)
-                t = mfma16f32(sm.Tm[16 * i + r16][16 * i + 4 * s4 + k4], sm.X[j][4 * s4 + k4][r16], t);
+                t = mfma16f32(sm.Tm[16 * i + r16][16 * i + 4 * k4 + s4], x[s4], t);
 #pragma unroll
             for (int r = 0; r < 4; ++r) sm.Tm[16 * i + 4 * k4 + r][16 * j + r16] = -t[r];
             wave_lds_sync();
