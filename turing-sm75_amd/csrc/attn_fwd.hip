@@ -4,7 +4,9 @@
 // keep running (m, l, O) per query row, O = O*alpha + P V, finally O / l.  The tiling is
 // CDNA4-shaped instead of a 16x16 warp tile:
 //   * a workgroup is 4 waves and owns 128 query rows (32 per wave); K/V tiles of 64 keys
-//     are double-buffered in LDS (64 KiB at D = 128) so two workgroups share a CU;
+//     are double-buffered in LDS (64 KiB at D = 128) so two workgroups share a CU, and
+//     copied there by LDS-DMA (global_load_lds_dwordx4, per-lane offsets computed once,
+//     the bank swizzle applied on the source side), so no register stages them;
 //   * each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_f16 (A = K rows from LDS,
 //     B = its 32 Q rows held in registers for the whole loop), so a lane owns one query
 //     and 16 keys per 32-key block: the row max / row sum are register reductions plus
@@ -12,10 +14,15 @@
 //   * P^T stays in registers (the S^T accumulator converted to fp16 is exactly the B
 //     operand layout of the next MFMA) and O^T += V^T P^T reads V^T straight out of the
 //     row-major V tile with ds_read_b64_tr_b16 -- no transpose pass;
-//   * softmax in the exp2 domain with scale*log2(e) folded into one FMA per score;
+//   * softmax in the exp2 domain with scale*log2(e) folded into one FMA per score; the
+//     running max used for the exponentials is raised only when a tile's max exceeds it
+//     by more than 2^8 (then O and l are rescaled), so most tiles skip the O rescale --
+//     exact, since O and l always share the same max, with P bounded by 2^8;
 //   * causal: tiles above a wave's diagonal are skipped, only diagonal / ragged tiles
 //     are masked; heavy (late) query tiles are scheduled first, and all query tiles of
 //     one (b, h) land on one XCD so its K/V stay in that XCD's L2.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -26,28 +33,32 @@ constexpr int kThreads = 256;
 constexpr int kQRows = 128;  // query rows per workgroup
 constexpr int kKRows = 64;   // keys per LDS tile
 
-// 16-byte chunk swizzle of an LDS tile row: chunk c of row r lives at c ^ swz(r).
-// swz is a permutation of r % 16, so 16 consecutive rows read at one chunk (the K
-// operand reads) hit 16 different bank groups, and for every aligned group of 4 rows
-// the values swz >> 1 differ, so the transposing V reads (4 rows x 2 chunks) do too.
+// 16-byte chunk swizzle of an LDS tile row: chunk c of row r lives at c ^ swz<D>(r).
+// LDS has 64 banks of 4 bytes; a 256-byte D = 128 row spans all of them, so a chunk's
+// banks depend on its position only.  The K operand reads (ds_read_b128, 16 lanes per
+// cycle) take 16 consecutive rows at one chunk: swz is a permutation of r % 16.  The
+// transposing V reads (ds_read_b64_tr_b16, 32 lanes per cycle) take 4 aligned rows x 4
+// chunks of one aligned chunk block: swz moves the 4 rows to 4 different chunk blocks.
+// At D = 64 two rows share the 64 banks and the other formula keeps both read patterns
+// conflict free.
+template <int D>
 __device__ __forceinline__ int swz(int r) {
-    return 2 * (r & 3) + ((r >> 2) & 1) + 8 * ((r >> 3) & 1);
+    if (D == 128) return 4 * (r & 3) + ((r >> 2) & 3);
+    return (2 * (r & 3) + ((r >> 2) & 1)) & 7;
 }
 
 template <int D>
 struct Cfg {
     static constexpr int kChunks = D / 8;                        // 16-B chunks per row
     static constexpr int kTile = kKRows * D;                     // halfs per K or V tile
-    static constexpr int kLoads = kKRows * kChunks / kThreads;   // 16-B loads per thread
     static constexpr int kKSteps = D / 16;                       // k-steps of S^T = K Q^T
     static constexpr int kDBlocks = D / 32;                      // 32-row blocks of O^T
     static constexpr int kLdsBytes = 2 * 2 * kTile * 2;          // 2 buffers x (K, V)
-    static_assert(kLoads * kThreads == kKRows * kChunks, "tile not covered");
 };
 
 template <int D>
 __device__ __forceinline__ int chunk_pos(int r, int c) {
-    return c ^ (swz(r) & (D / 8 - 1));
+    return c ^ swz<D>(r);
 }
 
 // Map the linear workgroup id to (bh, query tile).  Workgroups are dispatched round
@@ -67,31 +78,63 @@ __device__ __forceinline__ void map_block(int bid, int BH, int n_qt, bool causal
     qt = causal ? (n_qt - 1 - rank) : rank;
 }
 
-template <int D>
-__device__ __forceinline__ void load_tile(const half_t* __restrict__ src, int k0, int S,
-                                          uint4 (&reg)[Cfg<D>::kLoads]) {
-    const int tid = threadIdx.x;
-    const bool full = k0 + kKRows <= S;
-#pragma unroll
-    for (int it = 0; it < Cfg<D>::kLoads; ++it) {
-        const int id = it * kThreads + tid;
-        const int row = id / Cfg<D>::kChunks, c = id % Cfg<D>::kChunks;
-        if (full || k0 + row < S)
-            reg[it] = *reinterpret_cast<const uint4*>(src + (size_t)(k0 + row) * D + c * 8);
-        else
-            reg[it] = make_uint4(0, 0, 0, 0);
-    }
-}
+typedef __attribute__((address_space(3))) void* lds_void_t;
 
+// K/V tile copy plan.  One LDS-DMA instruction moves 1 KiB (lane l: 16 bytes to M0 + 16*l);
+// a tile of 64 rows x D halfs is kDmaTile instructions, K then V, and wave w issues
+// instructions w + 4j.  LDS chunk position p of row r holds source chunk p ^ swz(r), so
+// the tile lands in the same swizzled layout the operand reads expect.
 template <int D>
-__device__ __forceinline__ void store_tile(half_t* dst, const uint4 (&reg)[Cfg<D>::kLoads]) {
-    const int tid = threadIdx.x;
+struct Dma {
+    static constexpr int kTile = kKRows * D * 2 / 1024;  // instructions per K (or V) tile
+    static constexpr int kPerWave = 2 * kTile / 4;
+    static constexpr int kChunks = D / 8;
+};
+template <int D>
+__device__ __forceinline__ unsigned dma_off(int blk, int lane, int lastrow) {
+    const int P = blk * 64 + lane;
+    const int row = P / Dma<D>::kChunks, cpos = P % Dma<D>::kChunks;
+    const int c = cpos ^ swz<D>(row);
+    return (unsigned)(min(row, lastrow) * D + c * 8) * 2u;
+}
+// src = base + off (64-bit base in SGPRs, 32-bit VGPR offset).  Inline asm on purpose:
+// the compiler does not track LDS written by DMA per buffer and would wait for every
+// copy in flight before the first LDS read of the other buffer; the kernel orders the
+// copies itself (vmcnt(0) and a barrier at the end of each tile).
+__device__ __forceinline__ void dma_issue(const void* base, unsigned off, unsigned lds_addr) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(off), "s"(base), "{m0}"(lds_addr)
+                 : "memory");
+}
+// This wave's share of the copies of K/V rows k0..k0+63 into the buffer at lds_buf, in
+// two halves (kPart 0: j < kPerWave/2, kPart 1: the rest) so each can be issued between
+// MFMAs.
+template <int D, int kPart>
+__device__ __forceinline__ void copy_tile(const unsigned (&off)[Dma<D>::kPerWave], int wave,
+                                          const half_t* Kh, const half_t* Vh, int k0, int S,
+                                          unsigned lds_buf) {
+    const int lane = threadIdx.x & 63;
+    const half_t* kb = Kh + (size_t)k0 * D;
+    const half_t* vb = Vh + (size_t)k0 * D;
+    const int lastrow = S - 1 - k0;
+    auto issue_all = [&](auto Ragged) {  // a ragged last tile clamps its rows to S - 1
 #pragma unroll
-    for (int it = 0; it < Cfg<D>::kLoads; ++it) {
-        const int id = it * kThreads + tid;
-        const int row = id / Cfg<D>::kChunks, c = id % Cfg<D>::kChunks;
-        *reinterpret_cast<uint4*>(dst + row * D + chunk_pos<D>(row, c) * 8) = reg[it];
-    }
+        for (int j = kPart * Dma<D>::kPerWave / 2; j < (kPart + 1) * Dma<D>::kPerWave / 2; ++j) {
+            const int n = wave + 4 * j;  // wave is uniform; n < 2 * kTile
+            const bool isv = n >= Dma<D>::kTile;
+            const int blk = isv ? n - Dma<D>::kTile : n;
+            const unsigned o = decltype(Ragged)::value ? dma_off<D>(blk, lane, lastrow) : off[j];
+            dma_issue(isv ? (const void*)vb : (const void*)kb, o,
+                      lds_buf + (unsigned)(isv ? kKRows * D * 2 : 0) + 1024u * blk);
+        }
+    };
+    if (lastrow >= kKRows - 1)
+        issue_all(std::false_type{});
+    else
+        issue_all(std::true_type{});
+}
+__device__ __forceinline__ void dma_wait_barrier() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies have landed
+    lds_barrier();
 }
 
 template <int D, bool kCausal>
@@ -103,7 +146,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     extern __shared__ __align__(16) half_t lds[];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hi = lane >> 5;  // which half of the wave
     int bh, qt;
     map_block(blockIdx.x, BH, n_qt, kCausal, bh, qt);
@@ -130,47 +173,58 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     float16_t o[C::kDBlocks];
 #pragma unroll
     for (int i = 0; i < C::kDBlocks; ++i) o[i] = float16_t{};
-    float m = -INFINITY;  // running max of raw scores (q . k), per query
+    float m = -INFINITY;  // max of raw scores (q . k) the exponentials are taken against
     float l = 0.f;        // running sum of this lane's half of the keys
 
     // Lane-constant parts of the LDS addresses.
     const int krow = lane & 31;            // K operand row within a 32-key block
-    const int ksw = swz(krow) & (D / 8 - 1);
+    const int ksw = swz<D>(krow);
     const int g16 = lane >> 4, i16 = lane & 15;
     const int vj = i16 >> 2, vm = i16 & 3;  // transposed-read source row / column group
     // V^T operand: source row 16*ks + 8*e + 4*hi + vj, columns 32*db + 16*(g16&1) + 4*vm.
     const int vchunk = 2 * (g16 & 1) + (vm >> 1);
     const int vsub = 4 * (vm & 1);
 
-    uint4 kreg[C::kLoads], vreg[C::kLoads];
-    load_tile<D>(K + head, 0, S, kreg);
-    load_tile<D>(V + head, 0, S, vreg);
-    store_tile<D>(lds, kreg);
-    store_tile<D>(lds + C::kTile, vreg);
-    __syncthreads();
+    unsigned off[Dma<D>::kPerWave];
+#pragma unroll
+    for (int j = 0; j < Dma<D>::kPerWave; ++j) {
+        const int n = wave + 4 * j;
+        off[j] = dma_off<D>(n >= Dma<D>::kTile ? n - Dma<D>::kTile : n, lane, kKRows - 1);
+    }
+    const unsigned lds0 = (unsigned)(uintptr_t)(lds_void_t)(void*)lds;
+    const unsigned buf_bytes = 2 * C::kTile * 2;
+    copy_tile<D, 0>(off, wave, K + head, V + head, 0, S, lds0);
+    copy_tile<D, 1>(off, wave, K + head, V + head, 0, S, lds0);
+    dma_wait_barrier();
 
     for (int t = 0; t < n_tiles; ++t) {
         const int k0 = t * kKRows;
         const bool more = t + 1 < n_tiles;
-        if (more) {
-            load_tile<D>(K + head, k0 + kKRows, S, kreg);
-            load_tile<D>(V + head, k0 + kKRows, S, vreg);
-        }
-        if (k0 < wave_kv_end) {
+        const unsigned nbuf = lds0 + ((t + 1) & 1) * buf_bytes;
+        if (k0 >= wave_kv_end) {  // this wave's queries end before the tile: copies only
+            if (more) {
+                copy_tile<D, 0>(off, wave, K + head, V + head, k0 + kKRows, S, nbuf);
+                copy_tile<D, 1>(off, wave, K + head, V + head, k0 + kKRows, S, nbuf);
+            }
+        } else {
             const half_t* Kt = lds + (t & 1) * 2 * C::kTile;
             const half_t* Vt = Kt + C::kTile;
-            // ---- S^T = K Q^T for two 32-key blocks ----
-            float16_t s[2];
+            // ---- S^T = K Q^T for two 32-key blocks, the two accumulator chains interleaved ----
+            float16_t s[2] = {float16_t{}, float16_t{}};
+            const half_t* kr0 = Kt + krow * D;
+            const half_t* kr1 = kr0 + 32 * D;
+            __builtin_amdgcn_s_setprio(1);  // keep the matrix pipe fed while the other wave does VALU
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                s[kb] = float16_t{};
-                const half_t* kr = Kt + (kb * 32 + krow) * D;
-#pragma unroll
-                for (int kk = 0; kk < C::kKSteps; ++kk) {
-                    const half8_t a = *reinterpret_cast<const half8_t*>(kr + (((2 * kk + hi) ^ ksw) * 8));
-                    s[kb] = mfma32(a, qf[kk], s[kb]);
-                }
+            for (int kk = 0; kk < C::kKSteps; ++kk) {
+                const int cofs = ((2 * kk + hi) ^ ksw) * 8;
+                const half8_t a0 = *reinterpret_cast<const half8_t*>(kr0 + cofs);
+                const half8_t a1 = *reinterpret_cast<const half8_t*>(kr1 + cofs);
+                s[0] = mfma32(a0, qf[kk], s[0]);
+                s[1] = mfma32(a1, qf[kk], s[1]);
+                if (kk == C::kKSteps / 2 - 1 && more)
+                    copy_tile<D, 0>(off, wave, K + head, V + head, k0 + kKRows, S, nbuf);
             }
+            __builtin_amdgcn_s_setprio(0);
             // ---- masks: causal diagonal and keys past S ----
             if ((kCausal && k0 + kKRows - 1 > qw0) || k0 + kKRows > S) {
 #pragma unroll
@@ -188,29 +242,38 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m, mx);
-            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-            const float alpha = fast_exp2((m - m_use) * c2);
-            m = m_new;
-            const float mc = m_use * c2;
+            // Raise the reference max only when some score would exceed it by 2^8 in the
+            // exp2 domain (always on the first unmasked tile: m = -inf).
+            if (__builtin_amdgcn_ballot_w64((mx - m) * c2 > 8.f)) {
+                const float m_new = fmaxf(m, mx);
+                const float alpha = m_new == -INFINITY ? 1.f : fast_exp2((m - m_new) * c2);
+                m = m_new;
+                l *= alpha;
+#pragma unroll
+                for (int db = 0; db < C::kDBlocks; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+            }
+            const float mc = m == -INFINITY ? 0.f : m * c2;
             half8_t p[4];
-            float rs = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float pv = fast_exp2(fmaf(s[kb][r], c2, -mc));
-                    rs += pv;
-                    p[2 * kb + (r >> 3)][r & 7] = (half_t)pv;
-                }
-            l = fmaf(l, alpha, rs);
+                for (int r = 0; r < 16; ++r)
+                    p[2 * kb + (r >> 3)][r & 7] = (half_t)fast_exp2(fmaf(s[kb][r], c2, -mc));
+            // row sum of the fp16 P that multiplies V, on v_dot2_f32_f16
+            const half2_t one2 = {(half_t)1.f, (half_t)1.f};
 #pragma unroll
-            for (int db = 0; db < C::kDBlocks; ++db)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                for (int u = 0; u < 4; ++u)
+                    l = __builtin_amdgcn_fdot2(half2_t{p[i][2 * u], p[i][2 * u + 1]}, one2, l, false);
             // ---- O^T += V^T P^T ----
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
+                if (ks == 1 && more)
+                    copy_tile<D, 1>(off, wave, K + head, V + head, k0 + kKRows, S, nbuf);
 #pragma unroll
                 for (int db = 0; db < C::kDBlocks; ++db) {
                     const int r0 = 16 * ks + 4 * hi + vj;      // e = 0 row
@@ -222,13 +285,9 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                     o[db] = mfma32(a, p[ks], o[db]);
                 }
             }
+            __builtin_amdgcn_s_setprio(0);
         }
-        if (more) {
-            half_t* nxt = lds + ((t + 1) & 1) * 2 * C::kTile;
-            store_tile<D>(nxt, kreg);
-            store_tile<D>(nxt + C::kTile, vreg);
-        }
-        __syncthreads();
+        dma_wait_barrier();
     }
 
     // ---- epilogue: O = O^T / l, 4 consecutive d per store ----

@@ -6,6 +6,7 @@
 namespace tsa {
 
 typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
