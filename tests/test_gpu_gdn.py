@@ -151,6 +151,16 @@ def test_config5_decode_512_steps_subset(dev, orc):
     _check(o[sub], s[sub], o_ref, s_ref, 2e-3, 1e-5, label="decode 512 steps (3 seqs checked)")
 
 
+@pytest.mark.parametrize("B,Hq,Hv", [(1, 16, 32), (5, 16, 32), (16, 8, 16)])
+def test_decode_head_walk(dev, orc, B, Hq, Hv):
+    # B*Hv = 32, 160, 256: a decode workgroup walks 1, 2 or 4 column blocks of its head
+    rng = np.random.default_rng(505 + B)
+    q, k, v, g, beta, st = _inputs(rng, B, 4, Hq, Hv, sstd=0.02)
+    o, s = _decode_run(dev, q, k, v, g, beta, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    _check(o, s, o_ref, s_ref, 2e-3, 1e-5, label=f"decode B={B} Hv={Hv}")
+
+
 def test_recurrent_equals_decode_steps(dev):
     rng = np.random.default_rng(503)
     q, k, v, g, beta, st = _inputs(rng, 3, 9, 2, 4, sstd=0.02)
