@@ -152,8 +152,8 @@ def test_config5_decode_512_steps_subset(dev, orc):
 
 
 @pytest.mark.parametrize("B,Hq,Hv", [(1, 16, 32), (5, 16, 32), (16, 8, 16)])
-def test_decode_head_walk(dev, orc, B, Hq, Hv):
-    # B*Hv = 32, 160, 256: a decode workgroup walks 1, 2 or 4 column blocks of its head
+def test_decode_shapes(dev, orc, B, Hq, Hv):
+    # single sequences, odd batch counts, Hv = 2 Hq and Hv = Hq head maps
     rng = np.random.default_rng(505 + B)
     q, k, v, g, beta, st = _inputs(rng, B, 4, Hq, Hv, sstd=0.02)
     o, s = _decode_run(dev, q, k, v, g, beta, st)

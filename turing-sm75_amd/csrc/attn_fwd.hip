@@ -213,7 +213,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
             float16_t s[2] = {float16_t{}, float16_t{}};
             const half_t* kr0 = Kt + krow * D;
             const half_t* kr1 = kr0 + 32 * D;
-            __builtin_amdgcn_s_setprio(1);  // keep the matrix pipe fed while the other wave does VALU
+
 #pragma unroll
             for (int kk = 0; kk < C::kKSteps; ++kk) {
                 const int cofs = ((2 * kk + hi) ^ ksw) * 8;
@@ -224,7 +224,6 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                 if (kk == C::kKSteps / 2 - 1 && more)
                     copy_tile<D, 0>(off, wave, K + head, V + head, k0 + kKRows, S, nbuf);
             }
-            __builtin_amdgcn_s_setprio(0);
             // ---- masks: causal diagonal and keys past S ----
             if ((kCausal && k0 + kKRows - 1 > qw0) || k0 + kKRows > S) {
 #pragma unroll
@@ -268,7 +267,8 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
                     l = __builtin_amdgcn_fdot2(half2_t{p[i][2 * u], p[i][2 * u + 1]}, one2, l, false);
-            // ---- O^T += V^T P^T ----
+            // ---- O^T += V^T P^T (raised priority: the other wave of the SIMD is then mostly in
+            // its QK^T / softmax part, whose instructions fill the gaps between these MFMAs) ----
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {

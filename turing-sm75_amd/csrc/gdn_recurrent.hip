@@ -30,6 +30,7 @@ constexpr int kD = 128;          // dk = dv
 constexpr int kThreads = 256;
 constexpr int kColsPerBlock = kThreads / 8;  // 32
 constexpr int kBlocksPerHead = kD / kColsPerBlock;
+constexpr int kDecodeCols = 16;  // decode: columns per workgroup (8 threads per column)
 
 __device__ __forceinline__ void load_row16(const half_t* __restrict__ p, int j, float (&x)[16]) {
     // rows 4*(it*8 + j) .. +3 for it = 0..3
@@ -100,38 +101,38 @@ gdn_recurrent_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
     for (int it = 0; it < 4; ++it) __builtin_nontemporal_store(s[it], Sc + it * 8 + j);
 }
 
-// Decode step (T = 1).  A workgroup walks nblk consecutive 32-column blocks of one head:
-// q, k, g and beta are loaded once, and the next block's state is loaded while the current
-// block is updated and stored, so the state stream reads and writes overlap inside each
-// workgroup.  The q and k rows (512 bytes shared by every column) come in through LDS: one
-// wave loads them with one 8-byte load per lane instead of every thread issuing eight.
-// Same per-column math and lane layout as gdn_recurrent_kernel.
-__global__ void __launch_bounds__(kThreads)
+// Decode step (T = 1): one workgroup of 8 * kCols threads per kCols columns of a head, the
+// column layout of gdn_recurrent_kernel.  The q and k rows (512 bytes shared by every
+// column) come in through LDS: wave 0 loads them with one 8-byte load per lane instead of
+// every thread issuing eight.  Measured over 16 x 32 heads: 16 columns per workgroup
+// (4096 workgroups) beat 32 and 64, and walking several column blocks per workgroup with
+// the next block's state prefetched gained nothing.
+template <int kCols>
+__global__ void __launch_bounds__(8 * kCols)
 gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
                   const half_t* __restrict__ v, const float* __restrict__ g_log,
                   const float* __restrict__ beta, float* __restrict__ state,
-                  half_t* __restrict__ out, int Hq, int Hv, float scale, int nblk) {
-    const int wg_per_head = kBlocksPerHead / nblk;
-    const int bh = blockIdx.x / wg_per_head;
-    const int cb0 = (blockIdx.x % wg_per_head) * nblk;
+                  half_t* __restrict__ out, int Hq, int Hv, float scale) {
+    constexpr int kWgPerHead = kD / kCols;
+    const int bh = blockIdx.x / kWgPerHead;
     const int b = bh / Hv, h = bh % Hv, hq = h % Hq;
-    const int tid = threadIdx.x, j = tid & 7, cl = tid >> 3;
-    float4_t* Sh = reinterpret_cast<float4_t*>(state + (size_t)bh * kD * kD);
+    const int tid = threadIdx.x, j = tid & 7;
+    const int col = (blockIdx.x % kWgPerHead) * kCols + (tid >> 3);
     const size_t bt = (size_t)b;  // token index of sequence b (T = 1)
     const size_t vrow = (bt * Hv + h) * kD;
 
     __shared__ half4_t kq_rows[2][kD / 4];
-    float4_t s[4], sn[4];
-    {
-        const float4_t* Sc = Sh + (size_t)(cb0 * kColsPerBlock + cl) * (kD / 4);
+    float4_t* Sc = reinterpret_cast<float4_t*>(state + ((size_t)bh * kD + col) * kD);
+    float4_t s[4];
 #pragma unroll
-        for (int it = 0; it < 4; ++it) s[it] = __builtin_nontemporal_load(Sc + it * 8 + j);
-    }
-    if (tid < 64) {  // lanes 0-31: k row, 32-63: q row, 4 halfs each
+    for (int it = 0; it < 4; ++it) s[it] = __builtin_nontemporal_load(Sc + it * 8 + j);
+    if (tid < 64) {  // wave 0 -- lanes 0-31: k row, 32-63: q row, 4 halfs each
         const half_t* row = (tid < 32 ? k : q) + (bt * Hq + hq) * kD;
         kq_rows[tid >> 5][tid & 31] = *reinterpret_cast<const half4_t*>(row + 4 * (tid & 31));
     }
-    float vc = (float)v[vrow + cb0 * kColsPerBlock + cl];
+    const float vc = (float)v[vrow + col];
+    const float g = __expf(g_log[bt * Hv + h]);
+    const float be = beta[bt * Hv + h];
     __syncthreads();
     float kr[16], qr[16];
 #pragma unroll
@@ -143,46 +144,28 @@ gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
             qr[4 * it + e] = (float)hq4[e];
         }
     }
-    const float g = __expf(g_log[bt * Hv + h]);
-    const float be = beta[bt * Hv + h];
-    float kq = 0.f;
+    float kv = 0.f, sq = 0.f, kq = 0.f;
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            kv = fmaf(s[it][e], kr[4 * it + e], kv);
+            sq = fmaf(s[it][e], qr[4 * it + e], sq);
+        }
 #pragma unroll
     for (int i = 0; i < 16; ++i) kq = fmaf(kr[i], qr[i], kq);
+    kv = sum8(kv);
+    sq = sum8(sq);
     kq = sum8(kq);
-
-    for (int i = 0; i < nblk; ++i) {
-        const int col = (cb0 + i) * kColsPerBlock + cl;
-        float vn = 0.f;
-        if (i + 1 < nblk) {
-            const float4_t* Sn = Sh + (size_t)(col + kColsPerBlock) * (kD / 4);
+    const float d = (vc - g * kv) * be;
 #pragma unroll
-            for (int it = 0; it < 4; ++it) sn[it] = __builtin_nontemporal_load(Sn + it * 8 + j);
-            vn = (float)v[vrow + col + kColsPerBlock];
-        }
-        float kv = 0.f, sq = 0.f;
+    for (int it = 0; it < 4; ++it) {
+        float4_t x;
 #pragma unroll
-        for (int it = 0; it < 4; ++it)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                kv = fmaf(s[it][e], kr[4 * it + e], kv);
-                sq = fmaf(s[it][e], qr[4 * it + e], sq);
-            }
-        kv = sum8(kv);
-        sq = sum8(sq);
-        const float d = (vc - g * kv) * be;
-        float4_t* Sc = Sh + (size_t)col * (kD / 4);
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            float4_t x;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = fmaf(g, s[it][e], kr[4 * it + e] * d);
-            __builtin_nontemporal_store(x, Sc + it * 8 + j);
-        }
-        if (j == 0) out[vrow + col] = (half_t)(scale * fmaf(g, sq, d * kq));
-#pragma unroll
-        for (int it = 0; it < 4; ++it) s[it] = sn[it];
-        vc = vn;
+        for (int e = 0; e < 4; ++e) x[e] = fmaf(g, s[it][e], kr[4 * it + e] * d);
+        __builtin_nontemporal_store(x, Sc + it * 8 + j);
     }
+    if (j == 0) out[vrow + col] = (half_t)(scale * fmaf(g, sq, d * kq));
 }
 
 // Naive check kernel: one thread per state column, gdn_cpu order (src/gdn_sm75.cu:1090-1102).
@@ -223,13 +206,11 @@ hipError_t gdn_recurrent(const void* q, const void* k, const void* v, const floa
                          const float* beta, float* state, void* out, int B, int T, int Hq,
                          int Hv, float scale, hipStream_t stream) {
     if (T == 1) {
-        // two column blocks per workgroup when there are enough heads to fill the GPU
-        const int nblk = B * Hv >= 128 ? 2 : 1;
-        const unsigned blocks = (unsigned)(B * Hv * (kBlocksPerHead / nblk));
-        hipLaunchKernelGGL(gdn_decode_kernel, dim3(blocks), dim3(kThreads), 0, stream,
-                           static_cast<const half_t*>(q), static_cast<const half_t*>(k),
+        const unsigned blocks = (unsigned)(B * Hv * (kD / kDecodeCols));
+        hipLaunchKernelGGL(gdn_decode_kernel<kDecodeCols>, dim3(blocks), dim3(8 * kDecodeCols), 0,
+                           stream, static_cast<const half_t*>(q), static_cast<const half_t*>(k),
                            static_cast<const half_t*>(v), g_log, beta, state,
-                           static_cast<half_t*>(out), Hq, Hv, scale, nblk);
+                           static_cast<half_t*>(out), Hq, Hv, scale);
         return hipGetLastError();
     }
     const unsigned blocks = (unsigned)(B * Hv * kBlocksPerHead);
