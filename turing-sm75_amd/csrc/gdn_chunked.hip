@@ -446,71 +446,92 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
 }
 
 
+// Per-lane LDS offsets (in halfs, within a tile) of the chain step's operand reads.  The
+// swizzle makes them lane-dependent, but row-tile and slot steps are constant, so with
+// these bases every read in the loop is a base register plus an immediate.
+struct ChainOffs {
+    int w[4];   // W operand, k-step kk, row tile 0 (row tile mt adds 16 * mt * kD)
+    int k[8];   // K^T operand, row tile m of S, token rows 4g.. (token block ks adds 32*ks*kD)
+};
+__device__ __forceinline__ ChainOffs chain_offs() {
+    const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15, i16 = lane & 15;
+    ChainOffs o;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) o.w[kk] = tile_off(c, 4 * kk + g);
+    const int r = 4 * g + (i16 >> 2);  // token row this lane supplies to the transposed read
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int col = 16 * m + 4 * (i16 & 3);
+        o.k[m] = tile_off(r, col >> 3) + (col & 7);
+    }
+    return o;
+}
+
 // Chain step for one chunk: strip S (fp32 accumulators) <- next state, and the S / Vnew
-// operands handed to the output waves in XS.
-__device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs, uint4* xs, int sl) {
-    const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+// operands handed to the output waves in XS.  Every LDS read of the step (W and K^T
+// operands, U, decay factors) depends only on the chunk's slot, so all of them are issued
+// before the first MFMA and a scheduling barrier keeps them there: the MFMAs then find
+// their operands arriving in order instead of waiting on each small batch.
+__device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs, uint4* xs, int sl,
+                                           const ChainOffs& off) {
+    const int lane = threadIdx.x & 63, g = lane >> 4;
+    half8_t aW[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+            aW[mt][kk] = *reinterpret_cast<const half8_t*>(cs.W + off.w[kk] + 16 * mt * kD);
+    half4_t u[4];
+    float4 d4[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        u[mt] = *reinterpret_cast<const half4_t*>(cs.U + ((sl * 4 + mt) * 64 + lane) * 4);
+        d4[mt] = *reinterpret_cast<const float4*>(cs.Dg + 16 * mt + 4 * g);
+    }
+    const float eGC = cs.E[kC - 1];
+    // K^T operands of the state update, read transposed
+    half8_t aK[8][2];
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            aK[m][ks] = cat8(lds_read_tr16(cs.K + off.k[m] + 32 * ks * kD),
+                             lds_read_tr16(cs.K + off.k[m] + (32 * ks + 16) * kD));
+    __builtin_amdgcn_sched_barrier(0);
+
     half8_t Sb[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
         Sb[kk] = half8_t{(half_t)S[2 * kk][0], (half_t)S[2 * kk][1], (half_t)S[2 * kk][2], (half_t)S[2 * kk][3],
                          (half_t)S[2 * kk + 1][0], (half_t)S[2 * kk + 1][1], (half_t)S[2 * kk + 1][2], (half_t)S[2 * kk + 1][3]};
-    half4_t u[4];
-    float dg[4][4];
+    // W S, the four row-tile chains interleaved
+    float4_t wsv[4] = {float4_t{}, float4_t{}, float4_t{}, float4_t{}};
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        u[mt] = *reinterpret_cast<const half4_t*>(cs.U + ((sl * 4 + mt) * 64 + lane) * 4);
-        const float4 d4 = *reinterpret_cast<const float4*>(cs.Dg + 16 * mt + 4 * g);
-        dg[mt][0] = d4.x; dg[mt][1] = d4.y; dg[mt][2] = d4.z; dg[mt][3] = d4.w;
-    }
-    const float eGC = cs.E[kC - 1];
-    // W S in two batches of two row tiles; each batch's 8 W operands are read before its MFMAs
-    float4_t wsv[4];
+    for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-    for (int m0 = 0; m0 < 4; m0 += 2) {
-        half8_t aW[2][4];
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-                aW[mm][kk] = *reinterpret_cast<const half8_t*>(cs.W + tile_off(16 * (m0 + mm) + c, 4 * kk + g));
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm) {
-            wsv[m0 + mm] = float4_t{};
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) wsv[m0 + mm] = mfma16(aW[mm][kk], Sb[kk], wsv[m0 + mm]);
-        }
-    }
+        for (int mt = 0; mt < 4; ++mt) wsv[mt] = mfma16(aW[mt][kk], Sb[kk], wsv[mt]);
     // Vnew = U - W S (lane: column c, tokens 16mt + 4g + r); Vs = Vnew e^{G_C - G_t}
     half8_t Vn[2], Vs[2];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < 4; ++mt) {
+        const float dg[4] = {d4[mt].x, d4[mt].y, d4[mt].z, d4[mt].w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const float vn = (float)u[mt][r] - wsv[mt][r];
             Vn[mt >> 1][4 * (mt & 1) + r] = (half_t)vn;
-            Vs[mt >> 1][4 * (mt & 1) + r] = (half_t)(vn * dg[mt][r]);
+            Vs[mt >> 1][4 * (mt & 1) + r] = (half_t)(vn * dg[r]);
         }
+    }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) xs[kk * 64 + lane] = __builtin_bit_cast(uint4, Sb[kk]);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) xs[(4 + ks) * 64 + lane] = __builtin_bit_cast(uint4, Vn[ks]);
-    // S = e^{G_C} S + K^T Vs: K^T operands read transposed, 8 row tiles in two batches
+    // S = e^{G_C} S + K^T Vs
 #pragma unroll
-    for (int m0 = 0; m0 < 8; m0 += 4) {
-        half8_t aK[4][2];
+    for (int m = 0; m < 8; ++m) {
+        S[m] *= eGC;
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-                aK[mm][ks] = cat8(tile_read_tr(cs.K, 32 * ks + 4 * g, 16 * (m0 + mm)),
-                                  tile_read_tr(cs.K, 32 * ks + 16 + 4 * g, 16 * (m0 + mm)));
-#pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
-            S[m0 + mm] *= eGC;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) S[m0 + mm] = mfma16(aK[mm][ks], Vs[ks], S[m0 + mm]);
-        }
+        for (int ks = 0; ks < 2; ++ks) S[m] = mfma16(aK[m][ks], Vs[ks], S[m]);
     }
 }
 
@@ -537,22 +558,26 @@ __device__ __forceinline__ void out_step(const OutSlot& os, const uint4 (*xs)[6]
         const float4 e4 = *reinterpret_cast<const float4*>(os.E + 16 * (2 * w + j) + 4 * g);
         eg[j][0] = e4.x; eg[j][1] = e4.y; eg[j][2] = e4.z; eg[j][3] = e4.w;
     }
+    half8_t Sb[kStrips][4], Vn[kStrips][2];
+#pragma unroll
+    for (int s = 0; s < kStrips; ++s) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) Sb[s][kk] = __builtin_bit_cast(half8_t, xs[s][kk][lane]);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) Vn[s][ks] = __builtin_bit_cast(half8_t, xs[s][4 + ks][lane]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every LDS read of the step ahead of the MFMAs
     float4_t qs[2][kStrips], av[2][kStrips];
 #pragma unroll
     for (int s = 0; s < kStrips; ++s) {
-        half8_t Sb[4], Vn[2];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) Sb[kk] = __builtin_bit_cast(half8_t, xs[s][kk][lane]);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) Vn[ks] = __builtin_bit_cast(half8_t, xs[s][4 + ks][lane]);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             qs[j][s] = float4_t{};
             av[j][s] = float4_t{};
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) qs[j][s] = mfma16(aQ[j][kk], Sb[kk], qs[j][s]);
+            for (int kk = 0; kk < 4; ++kk) qs[j][s] = mfma16(aQ[j][kk], Sb[s][kk], qs[j][s]);
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) av[j][s] = mfma16(aA[j][ks], Vn[ks], av[j][s]);
+            for (int ks = 0; ks < 2; ++ks) av[j][s] = mfma16(aA[j][ks], Vn[s][ks], av[j][s]);
         }
     }
     // O tile (32 tokens x 32 columns) staged in LDS; out_flush stores it
@@ -619,11 +644,12 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
     // state occupies registers in another role's code.  `it` runs 0..nch; the loop is
     // unrolled by two so slot indices are constants.
     if (chain) {
+        const ChainOffs off = chain_offs();
         for (int it = 0; it <= nch; it += 2) {
-            if (it < nch) chain_step(S, sm.cs[0], &sm.XS[0][sl][0][0], sl);
+            if (it < nch) chain_step(S, sm.cs[0], &sm.XS[0][sl][0][0], sl, off);
             lds_barrier();  // chain waves issue no vector memory operations in the loop
             if (it + 1 > nch) break;
-            if (it + 1 < nch) chain_step(S, sm.cs[1], &sm.XS[1][sl][0][0], sl);
+            if (it + 1 < nch) chain_step(S, sm.cs[1], &sm.XS[1][sl][0][0], sl, off);
             lds_barrier();
         }
     } else if (outw) {
