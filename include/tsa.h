@@ -11,6 +11,8 @@
  * dtypes: q/k/v/o/out are IEEE fp16 (passed as void*), g_log, beta and the GDN state are
  * fp32.  Layouts follow the reference:
  *   attention : Q, K, V, O                [B][H][S][D]     (src/attn_sm75.cu:64,120,254)
+ *   grouped   : Q, gate, O [B][Hq][S][D]; K, V [B][Hkv][S][D]; query head h reads K/V
+ *               head h / (Hq / Hkv)
  *   GDN       : q, k                      [B][T][Hq][dk]   (src/gdn_sm75.cu:75-77)
  *               v, out                    [B][T][Hv][dv]
  *               g_log, beta               [B][T][Hv]
@@ -42,9 +44,10 @@ const char* tsa_version(void);
 
 /* Softmax flash-attention forward, O = softmax(scale * Q K^T [+ causal mask]) V.
  * Replaces launch_wmma<D> / launch_ffma<D> (src/attn_sm75.cu:421-440, dispatched on D at
- * :481-488) and its kernel flash_attn_sm75_wmma (:239-375).  D in {64, 128}; any S >= 1
- * (the reference caps S at 1024 for its naive check only, :457-460); causal 0 or 1 (the
- * reference hard-codes 1, :463).  fp32 softmax statistics, fp16 MFMA. */
+ * :481-488) and its kernel flash_attn_sm75_wmma (:239-375).  D in {64, 128} as the
+ * reference, and 256; any S >= 1 (the reference caps S at 1024 for its naive check only,
+ * :457-460); causal 0 or 1 (the reference hard-codes 1, :463).  fp32 softmax statistics,
+ * fp16 MFMA. */
 int tsa_attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
                  int D, float scale, int causal, void* stream);
 
@@ -54,6 +57,20 @@ int tsa_attn_fwd(const void* q, const void* k, const void* v, void* o, int B, in
  * its S <= 1024 threads-per-block limit.  Used by the attn_sm75 driver's error check. */
 int tsa_attn_naive(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
                    int D, float scale, int causal, void* stream);
+
+/* Gated grouped-query attention: O = softmax(scale * Q K^T [+ causal mask]) V, then
+ * O *= sigmoid(gate) element-wise when gate is not NULL.  The attention layer of the
+ * reference's target model (24 query / 4 K/V heads, head_dim 256, gate after softmax,
+ * docs/qwen38-27b.md:13), which the reference's lab does not implement (:19); no
+ * reference kernel is replaced.  Hq % Hkv == 0; D in {64, 128, 256}; q/k are taken after
+ * any rotary embedding.  tsa_attn_fwd is this call with Hkv = Hq and no gate. */
+int tsa_attn_gqa_fwd(const void* q, const void* k, const void* v, const void* gate, void* o,
+                     int B, int Hq, int Hkv, int S, int D, float scale, int causal,
+                     void* stream);
+/* The same on the naive check kernel (one thread per query row, exact two-pass softmax). */
+int tsa_attn_gqa_naive(const void* q, const void* k, const void* v, const void* gate, void* o,
+                       int B, int Hq, int Hkv, int S, int D, float scale, int causal,
+                       void* stream);
 
 /* Chunked Gated DeltaNet prefill over T tokens for B sequences, state carried in place.
  * Replaces the chunked kernels gdn_wmma_kernel (src/gdn_sm75.cu:361-574),

@@ -125,6 +125,29 @@ def attn_rows(q, k, v, rows, causal: bool, scale: float | None = None, nthreads=
     return rows, o32, o16.view(np.float16)
 
 
+def attn_gqa_rows(q, k, v, gate, rows, causal: bool, scale: float | None = None, nthreads=None):
+    """Gated grouped-query attention for the listed flat rows (bh*S + q of q's [B,Hq,S,D]).
+
+    Not a reference routine: the attention layer of the reference's target model (query
+    head h reads K/V head h // (Hq // Hkv), output times sigmoid(gate), docs/qwen38-27b.md:13)
+    defined on top of the pinned attention oracle: K/V repeated per query-head group, then
+    the gate applied in float64.  Returns (rows, float64 [n, D])."""
+    q, k, v = _as_h16(q), _as_h16(k), _as_h16(v)
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    assert Hq % Hkv == 0 and k.shape == (B, Hkv, S, D) and v.shape == k.shape
+    grp = Hq // Hkv
+    kr = np.ascontiguousarray(np.repeat(k, grp, axis=1))
+    vr = np.ascontiguousarray(np.repeat(v, grp, axis=1))
+    rows, o32, _ = attn_rows(q, kr, vr, rows, causal, scale, nthreads)
+    o = o32.astype(np.float64)
+    if gate is not None:
+        gf = np.asarray(gate, dtype=np.float64).reshape(-1, D)[rows]
+        with np.errstate(over="ignore"):  # exp(-g) = inf for very negative g: sigmoid 0
+            o = o / (1.0 + np.exp(-gf))
+    return rows, o
+
+
 def _gdn_prep(q, k, v, g, b, state):
     f = lambda a: np.ascontiguousarray(a, dtype=np.float32)
     q, k, v, g, b = f(q), f(k), f(v), f(g), f(b)

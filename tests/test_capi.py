@@ -45,7 +45,7 @@ def test_attn_argument_errors():
     assert _attn(S=0) == tsa.TSA_ERR_SHAPE
     assert _attn(B=-1) == tsa.TSA_ERR_SHAPE
     assert _attn(D=96) == tsa.TSA_ERR_UNSUPPORTED
-    assert _attn(D=256) == tsa.TSA_ERR_UNSUPPORTED
+    assert _attn(D=512) == tsa.TSA_ERR_UNSUPPORTED
     assert _attn(causal=2) == tsa.TSA_ERR_ARG
     assert _attn(scale=0.0) == tsa.TSA_ERR_ARG
     assert _attn(scale=-0.1) == tsa.TSA_ERR_ARG
@@ -53,6 +53,25 @@ def test_attn_argument_errors():
     assert _attn(B=1 << 16, H=1 << 16, S=1) == tsa.TSA_ERR_SHAPE
     lib = tsa.load()
     assert lib.tsa_attn_naive(DUMMY, DUMMY, NULL, DUMMY, 1, 1, 4, 64, 0.1, 0, NULL) == tsa.TSA_ERR_NULL
+
+
+def _gqa(*, q=DUMMY, gate=NULL, B=1, Hq=24, Hkv=4, S=16, D=256, scale=0.1, causal=1):
+    return tsa.load().tsa_attn_gqa_fwd(q, DUMMY, DUMMY, gate, DUMMY, B, Hq, Hkv, S, D, scale,
+                                       causal, NULL)
+
+
+def test_attn_gqa_argument_errors():
+    # gate may be NULL; every other pointer is required
+    assert _gqa(q=NULL) == tsa.TSA_ERR_NULL
+    assert _gqa(Hkv=5) == tsa.TSA_ERR_SHAPE    # 24 % 5 != 0
+    assert _gqa(Hkv=0) == tsa.TSA_ERR_SHAPE
+    assert _gqa(Hkv=48) == tsa.TSA_ERR_SHAPE   # more K/V heads than query heads
+    assert _gqa(D=96) == tsa.TSA_ERR_UNSUPPORTED
+    assert _gqa(causal=3) == tsa.TSA_ERR_ARG
+    assert _gqa(scale=float("inf")) == tsa.TSA_ERR_ARG
+    lib = tsa.load()
+    assert lib.tsa_attn_gqa_naive(DUMMY, NULL, DUMMY, NULL, DUMMY, 1, 2, 1, 4, 64, 0.1, 0,
+                                  NULL) == tsa.TSA_ERR_NULL
 
 
 def _chunked(*, T=64, Hv=2, dk=128, dv=128, chunk=64, ws=DUMMY, ws_bytes=1 << 30, st=DUMMY):

@@ -138,3 +138,69 @@ def test_stream_argument(dev, orc):
         o = tsa.attn_fwd(tq, tk, tv, causal=True, stream=s)
     s.synchronize()
     assert _err(o.cpu().numpy(), orc.attn_naive(q, k, v, True)) < TIGHT
+
+
+# ---- D = 256 and gated grouped-query attention (tsa_attn_gqa_fwd) ----
+def _run_gqa(dev, q, k, v, gate, causal, naive=False):
+    import torch
+    tq, tk, tv = _to_dev(dev, q, k, v)
+    tg = _to_dev(dev, gate)[0] if gate is not None else None
+    o = tsa.attn_gqa_fwd(tq, tk, tv, tg, causal=causal, naive=naive)
+    torch.cuda.synchronize()
+    return o.cpu().numpy()
+
+
+@pytest.mark.parametrize("S", [1, 64, 130, 300])
+@pytest.mark.parametrize("causal", [False, True])
+def test_d256(dev, orc, S, causal):
+    rng = np.random.default_rng(800 + S + causal)
+    q, k, v = (_normal(rng, (1, 2, S, 256)) for _ in range(3))
+    e = _err(_run(dev, q, k, v, causal), orc.attn_naive(q, k, v, causal))
+    print(f"D=256 S={S} causal={causal} max-abs {e:.5f}")
+    assert e < TIGHT
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [(1, 24, 4, 200, 256, True), (2, 6, 2, 129, 128, False),
+                                                (1, 4, 1, 65, 64, True), (1, 8, 8, 100, 128, True)])
+def test_gated_gqa(dev, orc, B, Hq, Hkv, S, D, causal):
+    rng = np.random.default_rng(810 + Hq + D + S)
+    q = _normal(rng, (B, Hq, S, D))
+    k, v = _normal(rng, (B, Hkv, S, D)), _normal(rng, (B, Hkv, S, D))
+    gate = _normal(rng, (B, Hq, S, D), 2.0)
+    o = _run_gqa(dev, q, k, v, gate, causal)
+    rows, ref = orc.attn_gqa_rows(q, k, v, gate, np.arange(B * Hq * S), causal)
+    e = _err(o.reshape(-1, D)[rows], ref)
+    en = _err(_run_gqa(dev, q, k, v, gate, causal, naive=True).reshape(-1, D)[rows], ref)
+    print(f"gated GQA {B}x{Hq}/{Hkv} S={S} D={D} max-abs {e:.5f} (naive kernel {en:.5f})")
+    assert e < TIGHT and en < 2e-3
+
+
+def test_gqa_without_gate_equals_attn_fwd(dev):
+    # Hkv = Hq and no gate is tsa_attn_fwd: the same kernel, bit-identical output
+    rng = np.random.default_rng(820)
+    q, k, v = (_normal(rng, (1, 4, 257, 128)) for _ in range(3))
+    o1 = _run(dev, q, k, v, True)
+    o2 = _run_gqa(dev, q, k, v, None, True)
+    assert np.array_equal(o1.view(np.uint16), o2.view(np.uint16))
+
+
+def test_gated_gqa_target_layer(dev, orc):
+    """The target model's gated attention layer at an 8K prefill: B=1, 24 query / 4 K/V
+    heads, D=256, causal, N(0, 0.5) inputs, gate N(0, 1); a seeded sample of rows against
+    the oracle and the full output against the on-device naive kernel."""
+    import torch
+    rng = np.random.default_rng(830)
+    B, Hq, Hkv, S, D = 1, 24, 4, 8192, 256
+    q = _normal(rng, (B, Hq, S, D), 0.5)
+    k, v = _normal(rng, (B, Hkv, S, D), 0.5), _normal(rng, (B, Hkv, S, D), 0.5)
+    gate = _normal(rng, (B, Hq, S, D))
+    tq, tk, tv, tg = _to_dev(dev, q, k, v, gate)
+    o = tsa.attn_gqa_fwd(tq, tk, tv, tg, causal=True)
+    on = tsa.attn_gqa_fwd(tq, tk, tv, tg, causal=True, naive=True)
+    torch.cuda.synchronize()
+    e_naive = float((o.float() - on.float()).abs().max())
+    rows = np.unique(np.concatenate([rng.integers(0, Hq * S, 96), [0, S - 1, 7 * S, 23 * S + S - 1]]))
+    rows, ref = orc.attn_gqa_rows(q, k, v, gate, rows, True)
+    e_orc = _err(o.cpu().numpy().reshape(-1, D)[rows], ref)
+    print(f"gated GQA 24/4 D=256 S=8192: max-abs vs naive kernel {e_naive:.5f}, vs oracle rows {e_orc:.5f}")
+    assert e_orc < TIGHT and e_naive < GATE

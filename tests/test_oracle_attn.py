@@ -106,3 +106,71 @@ def test_heads_are_independent(orc):
     o = orc.attn_naive(q, k, v, True)
     o1 = orc.attn_naive(q[1:2, 2:3].copy(), k[1:2, 2:3].copy(), v[1:2, 2:3].copy(), True)
     assert np.array_equal(o[1, 2].view(np.uint16), o1[0, 0].view(np.uint16))
+
+
+# ---- gated grouped-query attention (oracle.attn_gqa_rows) ----
+def _dense_gqa_f64(q, k, v, gate, causal, scale):
+    """Independent float64 dense softmax with an explicit K/V head map and gate."""
+    B, Hq, S, D = q.shape
+    grp = Hq // k.shape[1]
+    out = np.empty((B, Hq, S, D))
+    for b in range(B):
+        for h in range(Hq):
+            kk, vv = k[b, h // grp].astype(np.float64), v[b, h // grp].astype(np.float64)
+            s = scale * (q[b, h].astype(np.float64) @ kk.T)
+            if causal:
+                s = np.where(np.tril(np.ones((S, S), bool)), s, -np.inf)
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            o = (p / p.sum(axis=1, keepdims=True)) @ vv
+            if gate is not None:
+                o = o / (1.0 + np.exp(-gate[b, h].astype(np.float64)))
+            out[b, h] = o
+    return out
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,causal,gated", [(6, 1, 64, True, True), (4, 2, 128, False, True),
+                                                   (24, 4, 256, True, True), (3, 3, 64, True, False)])
+def test_gqa_matches_dense_f64(orc, Hq, Hkv, D, causal, gated):
+    rng = np.random.default_rng(700 + Hq + D)
+    B, S = 1, 37
+    q = rng.standard_normal((B, Hq, S, D)).astype(np.float16)
+    k = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
+    v = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
+    gate = rng.standard_normal((B, Hq, S, D)).astype(np.float16) if gated else None
+    rows = np.arange(B * Hq * S)
+    _, o = orc.attn_gqa_rows(q, k, v, gate, rows, causal)
+    ref = _dense_gqa_f64(q, k, v, gate, causal, 1.0 / np.sqrt(D)).reshape(-1, D)
+    assert np.abs(o - ref).max() < 1e-5
+
+
+def test_gqa_equal_heads_is_plain_attention(orc):
+    rng = np.random.default_rng(710)
+    q, k, v = (rng.standard_normal((1, 3, 50, 64)).astype(np.float16) for _ in range(3))
+    rows = np.arange(3 * 50)
+    _, o = orc.attn_gqa_rows(q, k, v, None, rows, True)
+    _, o32, _ = orc.attn_rows(q, k, v, rows, True)
+    assert np.array_equal(o, o32.astype(np.float64))
+
+
+def test_gqa_gate_closed_forms(orc):
+    rng = np.random.default_rng(711)
+    q = rng.standard_normal((1, 4, 20, 64)).astype(np.float16)
+    k, v = (rng.standard_normal((1, 2, 20, 64)).astype(np.float16) for _ in range(2))
+    rows = np.arange(4 * 20)
+    _, plain = orc.attn_gqa_rows(q, k, v, None, rows, False)
+    _, half = orc.attn_gqa_rows(q, k, v, np.zeros_like(q), rows, False)
+    _, closed = orc.attn_gqa_rows(q, k, v, np.full_like(q, -60000.0), rows, False)
+    assert np.allclose(half, plain / 2, rtol=0, atol=1e-12)   # sigmoid(0) = 1/2
+    assert np.abs(closed).max() < 1e-20                     # sigmoid(-60000) ~ 0
+
+
+def test_gqa_planted_head_map_error_is_caught(orc):
+    # a head map h % Hkv instead of h // (Hq // Hkv) must not pass the dense comparison
+    rng = np.random.default_rng(712)
+    q = rng.standard_normal((1, 4, 16, 64)).astype(np.float16)
+    k, v = (rng.standard_normal((1, 2, 16, 64)).astype(np.float16) for _ in range(2))
+    rows = np.arange(4 * 16)
+    _, o = orc.attn_gqa_rows(q, k, v, None, rows, True)
+    wrong = np.stack([k[0, h % 2] for h in range(4)])[None], np.stack([v[0, h % 2] for h in range(4)])[None]
+    _, o_wrong = orc.attn_gqa_rows(q, wrong[0], wrong[1], None, rows, True)
+    assert np.abs(o - o_wrong).max() > 0.1

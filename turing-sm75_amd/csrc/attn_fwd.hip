@@ -20,7 +20,12 @@
 //     exact, since O and l always share the same max, with P bounded by 2^8;
 //   * causal: tiles above a wave's diagonal are skipped, only diagonal / ragged tiles
 //     are masked; heavy (late) query tiles are scheduled first, and all query tiles of
-//     one (b, h) land on one XCD so its K/V stay in that XCD's L2.
+//     one (b, h) land on one XCD so its K/V stay in that XCD's L2;
+//   * grouped-query attention and the output gate of gated attention (the D = 256 layers
+//     of the reference's target model, docs/qwen38-27b.md:13): query head h reads K/V
+//     head h / (Hq / Hkv), and O is multiplied by sigmoid(gate) when a gate is given.
+//     At D = 256 a wave's 32 query rows need ~280 registers (Q operands 64, O^T 128), so
+//     the workgroup runs one wave per SIMD with the 128 KiB of K/V tiles to itself.
 #include <type_traits>
 
 #include "common.h"
@@ -43,7 +48,7 @@ constexpr int kKRows = 64;   // keys per LDS tile
 // conflict free.
 template <int D>
 __device__ __forceinline__ int swz(int r) {
-    if (D == 128) return 4 * (r & 3) + ((r >> 2) & 3);
+    if (D >= 128) return 4 * (r & 3) + ((r >> 2) & 3);  // D = 256: a row is two bank periods
     return (2 * (r & 3) + ((r >> 2) & 1)) & 7;
 }
 
@@ -138,9 +143,10 @@ __device__ __forceinline__ void dma_wait_barrier() {
 }
 
 template <int D, bool kCausal>
-__global__ void __launch_bounds__(kThreads, 2)
+__global__ void __launch_bounds__(kThreads, D == 256 ? 1 : 2)
 attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
-                const half_t* __restrict__ V, half_t* __restrict__ O, int S, int BH, int n_qt,
+                const half_t* __restrict__ V, const half_t* __restrict__ gate,
+                half_t* __restrict__ O, int S, int BH, int n_qt, int Hq, int group,
                 float c2 /* scale * log2(e) */) {
     using C = Cfg<D>;
     extern __shared__ __align__(16) half_t lds[];
@@ -150,7 +156,8 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const int hi = lane >> 5;  // which half of the wave
     int bh, qt;
     map_block(blockIdx.x, BH, n_qt, kCausal, bh, qt);
-    const size_t head = (size_t)bh * S * D;
+    const size_t head = (size_t)bh * S * D;  // Q, O, gate: query head bh = b * Hq + h
+    const size_t kvhead = (size_t)((bh / Hq) * (Hq / group) + (bh % Hq) / group) * S * D;
     const int q0 = qt * kQRows;
     const int qw0 = q0 + 32 * wave;
     const int my_q = qw0 + (lane & 31);
@@ -193,8 +200,8 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     }
     const unsigned lds0 = (unsigned)(uintptr_t)(lds_void_t)(void*)lds;
     const unsigned buf_bytes = 2 * C::kTile * 2;
-    copy_tile<D, 0>(off, wave, K + head, V + head, 0, S, lds0);
-    copy_tile<D, 1>(off, wave, K + head, V + head, 0, S, lds0);
+    copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, 0, S, lds0);
+    copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, 0, S, lds0);
     dma_wait_barrier();
 
     for (int t = 0; t < n_tiles; ++t) {
@@ -203,8 +210,8 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
         const unsigned nbuf = lds0 + ((t + 1) & 1) * buf_bytes;
         if (k0 >= wave_kv_end) {  // this wave's queries end before the tile: copies only
             if (more) {
-                copy_tile<D, 0>(off, wave, K + head, V + head, k0 + kKRows, S, nbuf);
-                copy_tile<D, 1>(off, wave, K + head, V + head, k0 + kKRows, S, nbuf);
+                copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
             }
         } else {
             const half_t* Kt = lds + (t & 1) * 2 * C::kTile;
@@ -222,7 +229,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                 s[0] = mfma32(a0, qf[kk], s[0]);
                 s[1] = mfma32(a1, qf[kk], s[1]);
                 if (kk == C::kKSteps / 2 - 1 && more)
-                    copy_tile<D, 0>(off, wave, K + head, V + head, k0 + kKRows, S, nbuf);
+                    copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
             }
             // ---- masks: causal diagonal and keys past S ----
             if ((kCausal && k0 + kKRows - 1 > qw0) || k0 + kKRows > S) {
@@ -273,7 +280,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 if (ks == 1 && more)
-                    copy_tile<D, 1>(off, wave, K + head, V + head, k0 + kKRows, S, nbuf);
+                    copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
 #pragma unroll
                 for (int db = 0; db < C::kDBlocks; ++db) {
                     const int r0 = 16 * ks + 4 * hi + vj;      // e = 0 row
@@ -290,53 +297,64 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
         dma_wait_barrier();
     }
 
-    // ---- epilogue: O = O^T / l, 4 consecutive d per store ----
+    // ---- epilogue: O = O^T / l (times sigmoid(gate)), 4 consecutive d per store ----
     l += __shfl_xor(l, 32);
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (my_q < S) {
         half_t* orow = O + head + (size_t)my_q * D;
+        const half_t* grow = gate ? gate + head + (size_t)my_q * D : nullptr;
 #pragma unroll
         for (int db = 0; db < C::kDBlocks; ++db)
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const half4_t v4 = {(half_t)(o[db][4 * rg] * inv), (half_t)(o[db][4 * rg + 1] * inv),
-                                    (half_t)(o[db][4 * rg + 2] * inv), (half_t)(o[db][4 * rg + 3] * inv)};
-                *reinterpret_cast<half4_t*>(orow + 32 * db + 8 * rg + 4 * hi) = v4;
+                const int d0 = 32 * db + 8 * rg + 4 * hi;
+                float f[4] = {inv, inv, inv, inv};
+                if (grow) {
+                    const half4_t g4 = *reinterpret_cast<const half4_t*>(grow + d0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) f[e] = inv / (1.f + __expf(-(float)g4[e]));
+                }
+                const half4_t v4 = {(half_t)(o[db][4 * rg] * f[0]), (half_t)(o[db][4 * rg + 1] * f[1]),
+                                    (half_t)(o[db][4 * rg + 2] * f[2]), (half_t)(o[db][4 * rg + 3] * f[3])};
+                *reinterpret_cast<half4_t*>(orow + d0) = v4;
             }
     }
 }
 
 template <int D, bool kCausal>
-hipError_t launch(const half_t* q, const half_t* k, const half_t* v, half_t* o, int B, int H,
-                  int S, float scale, hipStream_t stream) {
-    const int BH = B * H;
+hipError_t launch(const half_t* q, const half_t* k, const half_t* v, const half_t* gate, half_t* o,
+                  int B, int Hq, int Hkv, int S, float scale, hipStream_t stream) {
+    const int BH = B * Hq;
     const int n_qt = (S + kQRows - 1) / kQRows;
     const int lds = Cfg<D>::kLdsBytes;
     hipLaunchKernelGGL((attn_fwd_kernel<D, kCausal>), dim3(BH * n_qt), dim3(kThreads), lds,
-                       stream, q, k, v, o, S, BH, n_qt, scale * kLog2e);
+                       stream, q, k, v, gate, o, S, BH, n_qt, Hq, Hq / Hkv, scale * kLog2e);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------
-// Naive check kernel: one thread per query row (src/attn_sm75.cu:55-94 math).
+// Naive check kernel: one thread per query row (src/attn_sm75.cu:55-94 math), with the
+// grouped-query head map and the output gate of attn_fwd_kernel.
 // ---------------------------------------------------------------------------------
 template <int D>
 __global__ void __launch_bounds__(128)
 attn_naive_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
-                  const half_t* __restrict__ V, half_t* __restrict__ O, int S, long long rows,
-                  float scale, int causal) {
+                  const half_t* __restrict__ V, const half_t* __restrict__ gate,
+                  half_t* __restrict__ O, int S, int Hq, int group, long long rows, float scale,
+                  int causal) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= rows) return;
     const long long bh = idx / S;
     const int qi = (int)(idx % S);
     const size_t off = (size_t)bh * S * D;
+    const size_t kvoff = (size_t)((bh / Hq) * (Hq / group) + (bh % Hq) / group) * S * D;
     float qf[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) qf[d] = (float)Q[off + (size_t)qi * D + d];
     const int kend = causal ? qi + 1 : S;
     float m = -INFINITY;
     for (int kk = 0; kk < kend; ++kk) {
-        const half_t* kr = K + off + (size_t)kk * D;
+        const half_t* kr = K + kvoff + (size_t)kk * D;
         float dot = 0.f;
 #pragma unroll
         for (int d = 0; d < D; ++d) dot = fmaf(qf[d], (float)kr[d], dot);
@@ -347,49 +365,63 @@ attn_naive_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     for (int d = 0; d < D; ++d) acc[d] = 0.f;
     float l = 0.f;
     for (int kk = 0; kk < kend; ++kk) {
-        const half_t* kr = K + off + (size_t)kk * D;
+        const half_t* kr = K + kvoff + (size_t)kk * D;
         float dot = 0.f;
 #pragma unroll
         for (int d = 0; d < D; ++d) dot = fmaf(qf[d], (float)kr[d], dot);
         const float p = expf(fmaf(dot, scale, -m));
         l += p;
-        const half_t* vr = V + off + (size_t)kk * D;
+        const half_t* vr = V + kvoff + (size_t)kk * D;
 #pragma unroll
         for (int d = 0; d < D; ++d) acc[d] = fmaf(p, (float)vr[d], acc[d]);
     }
 #pragma unroll
-    for (int d = 0; d < D; ++d) O[off + (size_t)qi * D + d] = (half_t)(acc[d] / l);
+    for (int d = 0; d < D; ++d) {
+        float x = acc[d] / l;
+        if (gate) x *= 1.f / (1.f + expf(-(float)gate[off + (size_t)qi * D + d]));
+        O[off + (size_t)qi * D + d] = (half_t)x;
+    }
 }
 
 }  // namespace
 
-hipError_t attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
-                    int D, float scale, int causal, hipStream_t stream) {
+hipError_t attn_fwd(const void* q, const void* k, const void* v, const void* gate, void* o, int B,
+                    int Hq, int Hkv, int S, int D, float scale, int causal, hipStream_t stream) {
     auto Q = static_cast<const half_t*>(q);
     auto K = static_cast<const half_t*>(k);
     auto Vp = static_cast<const half_t*>(v);
+    auto G = static_cast<const half_t*>(gate);
     auto Op = static_cast<half_t*>(o);
+    if (D == 256)
+        return causal ? launch<256, true>(Q, K, Vp, G, Op, B, Hq, Hkv, S, scale, stream)
+                      : launch<256, false>(Q, K, Vp, G, Op, B, Hq, Hkv, S, scale, stream);
     if (D == 128)
-        return causal ? launch<128, true>(Q, K, Vp, Op, B, H, S, scale, stream)
-                      : launch<128, false>(Q, K, Vp, Op, B, H, S, scale, stream);
-    return causal ? launch<64, true>(Q, K, Vp, Op, B, H, S, scale, stream)
-                  : launch<64, false>(Q, K, Vp, Op, B, H, S, scale, stream);
+        return causal ? launch<128, true>(Q, K, Vp, G, Op, B, Hq, Hkv, S, scale, stream)
+                      : launch<128, false>(Q, K, Vp, G, Op, B, Hq, Hkv, S, scale, stream);
+    return causal ? launch<64, true>(Q, K, Vp, G, Op, B, Hq, Hkv, S, scale, stream)
+                  : launch<64, false>(Q, K, Vp, G, Op, B, Hq, Hkv, S, scale, stream);
 }
 
-hipError_t attn_naive(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
-                      int D, float scale, int causal, hipStream_t stream) {
-    const long long rows = (long long)B * H * S;
+hipError_t attn_naive(const void* q, const void* k, const void* v, const void* gate, void* o,
+                      int B, int Hq, int Hkv, int S, int D, float scale, int causal,
+                      hipStream_t stream) {
+    const long long rows = (long long)B * Hq * S;
     const unsigned blocks = (unsigned)((rows + 127) / 128);
     auto Q = static_cast<const half_t*>(q);
     auto K = static_cast<const half_t*>(k);
     auto Vp = static_cast<const half_t*>(v);
+    auto G = static_cast<const half_t*>(gate);
     auto Op = static_cast<half_t*>(o);
-    if (D == 128)
-        hipLaunchKernelGGL(attn_naive_kernel<128>, dim3(blocks), dim3(128), 0, stream, Q, K, Vp,
-                           Op, S, rows, scale, causal);
+    const int group = Hq / Hkv;
+    if (D == 256)
+        hipLaunchKernelGGL(attn_naive_kernel<256>, dim3(blocks), dim3(128), 0, stream, Q, K, Vp, G,
+                           Op, S, Hq, group, rows, scale, causal);
+    else if (D == 128)
+        hipLaunchKernelGGL(attn_naive_kernel<128>, dim3(blocks), dim3(128), 0, stream, Q, K, Vp, G,
+                           Op, S, Hq, group, rows, scale, causal);
     else
-        hipLaunchKernelGGL(attn_naive_kernel<64>, dim3(blocks), dim3(128), 0, stream, Q, K, Vp,
-                           Op, S, rows, scale, causal);
+        hipLaunchKernelGGL(attn_naive_kernel<64>, dim3(blocks), dim3(128), 0, stream, Q, K, Vp, G,
+                           Op, S, Hq, group, rows, scale, causal);
     return hipGetLastError();
 }
 

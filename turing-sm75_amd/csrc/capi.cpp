@@ -20,10 +20,12 @@ inline bool fits_int(long long a, long long b, long long c = 1) {
 }
 
 int check_attn(const void* q, const void* k, const void* v, const void* o, int B, int H, int S,
-               int D, float scale, int causal) {
+               int D, float scale, int causal, int Hkv = -1) {
     if (!q || !k || !v || !o) return TSA_ERR_NULL;
-    if (B < 1 || H < 1 || S < 1 || D < 1) return TSA_ERR_SHAPE;
-    if (D != 64 && D != 128) return TSA_ERR_UNSUPPORTED;
+    if (Hkv == -1) Hkv = H;
+    if (B < 1 || H < 1 || Hkv < 1 || S < 1 || D < 1) return TSA_ERR_SHAPE;
+    if (H % Hkv != 0) return TSA_ERR_SHAPE;
+    if (D != 64 && D != 128 && D != 256) return TSA_ERR_UNSUPPORTED;
     if (causal != 0 && causal != 1) return TSA_ERR_ARG;
     // The running max is taken over raw q.k, which is the max of the scaled scores only
     // for scale > 0 (the reference's scale is 1/sqrt(D), src/attn_sm75.cu:462).
@@ -51,7 +53,7 @@ extern "C" const char* tsa_strerror(int code) {
         case TSA_OK: return "ok";
         case TSA_ERR_NULL: return "a required pointer is NULL";
         case TSA_ERR_SHAPE: return "invalid shape (size < 1, too large, or inconsistent)";
-        case TSA_ERR_UNSUPPORTED: return "shape not supported by this build (attention: D in {64,128}; GDN: dk = dv = 128, chunk = 64)";
+        case TSA_ERR_UNSUPPORTED: return "shape not supported by this build (attention: D in {64,128,256}; GDN: dk = dv = 128, chunk = 64)";
         case TSA_ERR_WORKSPACE: return "workspace is NULL or smaller than the required size";
         case TSA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
         case TSA_ERR_ARG: return "invalid argument (causal not 0/1, or scale not finite / not > 0)";
@@ -65,14 +67,34 @@ extern "C" int tsa_attn_fwd(const void* q, const void* k, const void* v, void* o
                             int S, int D, float scale, int causal, void* stream) {
     const int rc = check_attn(q, k, v, o, B, H, S, D, scale, causal);
     if (rc) return rc;
-    return from_hip(tsa::attn_fwd(q, k, v, o, B, H, S, D, scale, causal, as_stream(stream)));
+    return from_hip(tsa::attn_fwd(q, k, v, nullptr, o, B, H, H, S, D, scale, causal,
+                                  as_stream(stream)));
 }
 
 extern "C" int tsa_attn_naive(const void* q, const void* k, const void* v, void* o, int B,
                               int H, int S, int D, float scale, int causal, void* stream) {
     const int rc = check_attn(q, k, v, o, B, H, S, D, scale, causal);
     if (rc) return rc;
-    return from_hip(tsa::attn_naive(q, k, v, o, B, H, S, D, scale, causal, as_stream(stream)));
+    return from_hip(tsa::attn_naive(q, k, v, nullptr, o, B, H, H, S, D, scale, causal,
+                                    as_stream(stream)));
+}
+
+extern "C" int tsa_attn_gqa_fwd(const void* q, const void* k, const void* v, const void* gate,
+                                void* o, int B, int Hq, int Hkv, int S, int D, float scale,
+                                int causal, void* stream) {
+    const int rc = check_attn(q, k, v, o, B, Hq, S, D, scale, causal, Hkv);
+    if (rc) return rc;
+    return from_hip(tsa::attn_fwd(q, k, v, gate, o, B, Hq, Hkv, S, D, scale, causal,
+                                  as_stream(stream)));
+}
+
+extern "C" int tsa_attn_gqa_naive(const void* q, const void* k, const void* v, const void* gate,
+                                  void* o, int B, int Hq, int Hkv, int S, int D, float scale,
+                                  int causal, void* stream) {
+    const int rc = check_attn(q, k, v, o, B, Hq, S, D, scale, causal, Hkv);
+    if (rc) return rc;
+    return from_hip(tsa::attn_naive(q, k, v, gate, o, B, Hq, Hkv, S, D, scale, causal,
+                                    as_stream(stream)));
 }
 
 extern "C" size_t tsa_gdn_chunked_workspace_bytes(int B, int T, int Hq, int Hv, int dk, int dv,

@@ -6,10 +6,12 @@
 
 namespace tsa {
 
-hipError_t attn_fwd(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
-                    int D, float scale, int causal, hipStream_t stream);
-hipError_t attn_naive(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
-                      int D, float scale, int causal, hipStream_t stream);
+// q, gate, o: [B][Hq][S][D]; k, v: [B][Hkv][S][D]; gate may be null; Hq % Hkv == 0.
+hipError_t attn_fwd(const void* q, const void* k, const void* v, const void* gate, void* o, int B,
+                    int Hq, int Hkv, int S, int D, float scale, int causal, hipStream_t stream);
+hipError_t attn_naive(const void* q, const void* k, const void* v, const void* gate, void* o,
+                      int B, int Hq, int Hkv, int S, int D, float scale, int causal,
+                      hipStream_t stream);
 
 size_t gdn_chunked_ws_bytes(int B, int T, int Hv);
 hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,

@@ -1,6 +1,7 @@
 // attn_sm75 -- the attention lab driver, rebuilt over the tsa C-ABI.
 //
 //   attn_sm75 [B H S D] [--causal 0|1] [--std X] [--outlier P] [--seed N] [--iters N]
+//             [--hkv N] [--gate 0|1]
 //
 // Mirrors main() of src/attn_sm75.cu:442-554: positional B H S D (default 2 8 512 128),
 // D in {64, 128} (usage error -> exit 2), scale 1/sqrt(D), std::mt19937(seed) with
@@ -10,15 +11,19 @@
 // causal-executed (2 B H S (S+1) D) conventions (:531-535), exit 0 iff the check passes.
 // Differences: causal is a flag (the reference hard-codes 1, :463) and S is not capped at
 // 1024 (the naive check here is O(S^2 D), not O(S^2 D^2)).  --outlier P multiplies each
-// element by 8 with probability P (independent mt19937(seed + 1) stream).
+// element by 8 with probability P (independent mt19937(seed + 1) stream).  D = 256 is
+// accepted as well.  --hkv N (H % N == 0) runs grouped-query attention with N K/V heads and
+// --gate 1 multiplies the output by sigmoid(gate), gate ~ N(0, 1) drawn after V: the gated
+// attention layer of the reference's target model (docs/qwen38-27b.md:13), through
+// tsa_attn_gqa_fwd and checked against tsa_attn_gqa_naive.
 #include "driver_util.h"
 
 int main(int argc, char** argv) {
     Opts opt(argc, argv);
     int B = 2, H = 8, S = 512, D = 128;
-    if (opt.bad || !opt.known({"causal", "std", "outlier", "seed", "iters"}) ||
+    if (opt.bad || !opt.known({"causal", "std", "outlier", "seed", "iters", "hkv", "gate"}) ||
         (opt.pos.size() != 0 && opt.pos.size() != 4)) {
-        std::fprintf(stderr, "usage: %s [B H S D] [--causal 0|1] [--std X] [--outlier P] [--seed N] [--iters N]\n", argv[0]);
+        std::fprintf(stderr, "usage: %s [B H S D] [--causal 0|1] [--std X] [--outlier P] [--seed N] [--iters N] [--hkv N] [--gate 0|1]\n", argv[0]);
         return 2;
     }
     if (opt.pos.size() == 4) {
@@ -32,42 +37,62 @@ int main(int argc, char** argv) {
     const double outlier = std::atof(opt.get("outlier", "0").c_str());
     const unsigned seed = (unsigned)std::strtoul(opt.get("seed", "42").c_str(), nullptr, 10);
     const int iters = std::atoi(opt.get("iters", "20").c_str());
-    if (D != 64 && D != 128) {
-        std::fprintf(stderr, "kernels instantiate D=64 and D=128 only\n");
+    const int Hkv = std::atoi(opt.get("hkv", std::to_string(H).c_str()).c_str());
+    const int gate_flag = std::atoi(opt.get("gate", "0").c_str());
+    const bool gated = gate_flag == 1;
+    if (D != 64 && D != 128 && D != 256) {
+        std::fprintf(stderr, "kernels instantiate D=64, D=128 and D=256 only\n");
         return 2;
     }
-    if (B < 1 || H < 1 || S < 1 || (causal != 0 && causal != 1) || iters < 1) {
+    if (B < 1 || H < 1 || S < 1 || Hkv < 1 || H % Hkv != 0 || (causal != 0 && causal != 1) ||
+        (gate_flag != 0 && gate_flag != 1) || iters < 1) {
         std::fprintf(stderr, "invalid shape or option\n");
         return 2;
     }
     const float scale = 1.f / std::sqrt((float)D);
     const size_t elems = (size_t)B * H * S * D;
+    const size_t kv_elems = (size_t)B * Hkv * S * D;
 
     print_gpu();
-    std::printf("shape           : B=%d H=%d S=%d D=%d  causal=%d\n", B, H, S, D, causal);
+    std::printf("shape           : B=%d H=%d S=%d D=%d  causal=%d", B, H, S, D, causal);
+    if (Hkv != H || gated) std::printf("  K/V heads=%d  gate=%d", Hkv, (int)gated);
+    std::printf("\n");
     std::printf("tile            : 128 q rows x 64 keys per LDS tile, 4 waves, v_mfma_f32_32x32x16_f16\n");
 
-    std::vector<f16> hq(elems), hk(elems), hv(elems);
+    std::vector<f16> hq(elems), hk(kv_elems), hv(kv_elems), hg(gated ? elems : 0);
     {
         std::mt19937 rng(seed);
         std::mt19937 rng_o(seed + 1);
         std::uniform_real_distribution<double> u01(0.0, 1.0);
         for (std::vector<f16>* t : {&hq, &hk, &hv}) {
             std::normal_distribution<float> dist(0.f, stdv);
-            for (size_t i = 0; i < elems; ++i) {
+            for (size_t i = 0; i < t->size(); ++i) {
                 float x = dist(rng);
                 if (outlier > 0 && u01(rng_o) < outlier) x *= 8.f;
                 (*t)[i] = (f16)x;
             }
         }
+        std::normal_distribution<float> gd(0.f, 1.f);
+        for (size_t i = 0; i < hg.size(); ++i) hg[i] = (f16)gd(rng);
     }
-    DevBuf<f16> Q(elems), K(elems), V(elems), Om(elems), On(elems);
+    DevBuf<f16> Q(elems), K(kv_elems), V(kv_elems), G(gated ? elems : 1), Om(elems), On(elems);
     Q.upload(hq);
     K.upload(hk);
     V.upload(hv);
+    if (gated) G.upload(hg);
+    const bool gqa = Hkv != H || gated;
+    const void* gp = gated ? G.d : nullptr;
+    auto run_mfma = [&] {
+        if (gqa) DRV_TSA(tsa_attn_gqa_fwd(Q.d, K.d, V.d, gp, Om.d, B, H, Hkv, S, D, scale, causal, nullptr));
+        else DRV_TSA(tsa_attn_fwd(Q.d, K.d, V.d, Om.d, B, H, S, D, scale, causal, nullptr));
+    };
+    auto run_naive = [&] {
+        if (gqa) DRV_TSA(tsa_attn_gqa_naive(Q.d, K.d, V.d, gp, On.d, B, H, Hkv, S, D, scale, causal, nullptr));
+        else DRV_TSA(tsa_attn_naive(Q.d, K.d, V.d, On.d, B, H, S, D, scale, causal, nullptr));
+    };
 
-    DRV_TSA(tsa_attn_fwd(Q.d, K.d, V.d, Om.d, B, H, S, D, scale, causal, nullptr));
-    DRV_TSA(tsa_attn_naive(Q.d, K.d, V.d, On.d, B, H, S, D, scale, causal, nullptr));
+    run_mfma();
+    run_naive();
     DRV_HIP(hipDeviceSynchronize());
     std::vector<f16> om, on;
     Om.download(om);
@@ -79,9 +104,9 @@ int main(int argc, char** argv) {
     }
     std::printf("max |mfma-naive| : %.5f   %s\n", err, err < 2e-2f ? "OK" : "FAIL");
 
-    const float mfma_ms = time_ms([&] { DRV_TSA(tsa_attn_fwd(Q.d, K.d, V.d, Om.d, B, H, S, D, scale, causal, nullptr)); }, iters);
+    const float mfma_ms = time_ms(run_mfma, iters);
     const int naive_iters = S > 2048 ? 1 : iters;
-    const float naive_ms = time_ms([&] { DRV_TSA(tsa_attn_naive(Q.d, K.d, V.d, On.d, B, H, S, D, scale, causal, nullptr)); }, naive_iters);
+    const float naive_ms = time_ms(run_naive, naive_iters);
 
     const double flops_dense = 4.0 * B * H * (double)S * S * D;
     const double flops_exec = causal ? 2.0 * B * H * (double)S * (S + 1.0) * D : flops_dense;

@@ -38,6 +38,8 @@ _SIGNATURES = {
     "tsa_version": (ctypes.c_char_p, []),
     "tsa_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp]),
     "tsa_attn_naive": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp]),
+    "tsa_attn_gqa_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp]),
+    "tsa_attn_gqa_naive": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp]),
     "tsa_gdn_chunked_workspace_bytes": (_sz, [_i] * 7),
     "tsa_gdn_chunked_fwd": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp, _sz, _vp]),
     "tsa_gdn_recurrent_fwd": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
@@ -129,6 +131,35 @@ def attn_fwd(q, k, v, out=None, scale=None, causal=True, stream=None, naive=Fals
     fn = load().tsa_attn_naive if naive else load().tsa_attn_fwd
     _check(fn(_ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, S, D, float(scale), int(bool(causal)),
               _stream(stream)))
+    return out
+
+
+def attn_gqa_fwd(q, k, v, gate=None, out=None, scale=None, causal=True, stream=None, naive=False):
+    """Gated grouped-query attention: q, gate [B, Hq, S, D]; k, v [B, Hkv, S, D] with
+    Hq % Hkv == 0; O = softmax(scale Q K^T [+ causal mask]) V, times sigmoid(gate) if given."""
+    import torch
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _need(t, torch.float16, 4, name)
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if k.shape != (B, Hkv, S, D) or v.shape != k.shape:
+        raise ValueError(f"k, v must be [B, Hkv, S, D] with q's B, S, D: {tuple(q.shape)} "
+                         f"{tuple(k.shape)} {tuple(v.shape)}")
+    if gate is not None:
+        _need(gate, torch.float16, 4, "gate")
+        if gate.shape != q.shape:
+            raise ValueError("gate shape differs from q")
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.float16, 4, "out")
+    if out.shape != q.shape:
+        raise ValueError("out shape differs from q")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    fn = load().tsa_attn_gqa_naive if naive else load().tsa_attn_gqa_fwd
+    gp = _ptr(gate) if gate is not None else ctypes.c_void_p(0)
+    _check(fn(_ptr(q), _ptr(k), _ptr(v), gp, _ptr(out), B, Hq, Hkv, S, D, float(scale),
+              int(bool(causal)), _stream(stream)))
     return out
 
 
