@@ -16,6 +16,9 @@ One bench step is one pass over the hot path with every input already resident i
     loop, not one launch's latency.
 W untimed warmup steps, then exactly K timed steps between two synchronisations.  Each
 kernel's average duration comes from HIP events recorded on the stream it runs on.
+After the timed steps, outside the step, the gated grouped-query attention layer of the
+reference's target model (B=1, 24 query / 4 K/V heads, D=256, S=8192, causal, gate after
+softmax) is timed on its own and reported as the part `attn_gqa_gated`.
 
 Printed: one JSON line.  `value` is the attention forward throughput (TFLOP/s, causal
 executed FLOPs 2*B*H*S*(S+1)*D, the convention of src/attn_sm75.cu:534), the kernel that
@@ -41,6 +44,8 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 
 # configuration of each part
 ATTN = dict(B=1, H=32, S=8192, D=128, causal=True)
+# the target model's gated attention layer (24 query / 4 K/V heads, head_dim 256)
+GQA = dict(B=1, Hq=24, Hkv=4, S=8192, D=256, causal=True)
 PREFILL = dict(B=1, T=4096, Hq=16, Hv=32, d=128, chunk=64)
 DECODE = dict(B=16, Hq=16, Hv=32, d=128, replicas=16)
 
@@ -120,6 +125,16 @@ def make_inputs(torch, dev, seed=2026):
     dec["states"] = [0.02 * torch.randn(d["B"], d["Hv"], d["d"], d["d"], device=dev, generator=gen)
                      for _ in range(d["replicas"])]
     dec["out"] = torch.empty_like(dec["v"])
+
+    g = GQA
+    gq = dict(
+        q=(0.5 * torch.randn(g["B"], g["Hq"], g["S"], g["D"], device=dev, generator=gen)).half(),
+        k=(0.5 * torch.randn(g["B"], g["Hkv"], g["S"], g["D"], device=dev, generator=gen)).half(),
+        v=(0.5 * torch.randn(g["B"], g["Hkv"], g["S"], g["D"], device=dev, generator=gen)).half(),
+        gate=torch.randn(g["B"], g["Hq"], g["S"], g["D"], device=dev, generator=gen).half(),
+    )
+    gq["o"] = torch.empty_like(gq["q"])
+    a["gqa"] = gq
     return a, pre, dec
 
 
@@ -128,9 +143,9 @@ def cpu_baselines(torch, a, pre, dec, threads):
     import numpy as np
     import oracle
     res = {}
-    # attention: every row of 8 of the 32 heads (causal), all host threads
+    # attention: every causal row of all 32 heads, all host threads
     s = ATTN
-    nh = 8
+    nh = s["H"]
     q, k, v = (a[n][:, :nh].cpu().numpy() for n in ("q", "k", "v"))
     rows = np.arange(nh * s["S"], dtype=np.int64)
     t0 = time.perf_counter()
@@ -139,6 +154,20 @@ def cpu_baselines(torch, a, pre, dec, threads):
     fl = attn_flops(1, nh, s["S"], s["D"], True)
     res["attn_fwd"] = {"value": fl / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
                        "sample": f"all {s['S']} causal rows of {nh} of {s['H']} heads ({dt:.1f} s)"}
+    # gated GQA layer: every row of the first query-head group (6 heads sharing K/V head 0)
+    c = GQA
+    gq = a["gqa"]
+    grp = c["Hq"] // c["Hkv"]
+    qn, gn = (gq[n][:, :grp].cpu().numpy() for n in ("q", "gate"))
+    kn, vn = (gq[n][:, :1].cpu().numpy() for n in ("k", "v"))
+    rows = np.arange(grp * c["S"], dtype=np.int64)
+    t0 = time.perf_counter()
+    oracle.attn_gqa_rows(qn, kn, vn, gn, rows, True, nthreads=threads)
+    dt = time.perf_counter() - t0
+    fl = attn_flops(1, grp, c["S"], c["D"], True)
+    res["attn_gqa_gated"] = {"value": fl / dt / 1e12, "unit": "TFLOP/s", "cores": threads,
+                             "kind": "port",
+                             "sample": f"all {c['S']} causal rows of {grp} of {c['Hq']} query heads ({dt:.1f} s)"}
     # prefill: serial recurrence, all 4096 tokens of all 32 V-heads
     p = PREFILL
     hv_s = 32
@@ -146,15 +175,17 @@ def cpu_baselines(torch, a, pre, dec, threads):
     qn, kn = g("q"), g("k")
     vn, bn, gn = g("v")[:, :, :hv_s], g("beta")[:, :, :hv_s], g("g")[:, :, :hv_s]
     st = np.zeros((1, hv_s, p["d"], p["d"]), np.float32)
+    reps = 10
     t0 = time.perf_counter()
-    oracle.gdn_serial(qn, kn, vn, gn, bn, st, nthreads=threads)
+    for _ in range(reps):
+        oracle.gdn_serial(qn, kn, vn, gn, bn, st, nthreads=threads)
     dt = time.perf_counter() - t0
-    tok_s = p["B"] * p["T"] / (dt * p["Hv"] / hv_s)
+    tok_s = reps * p["B"] * p["T"] / (dt * p["Hv"] / hv_s)
     res["gdn_prefill"] = {"value": tok_s, "unit": "tok/s", "cores": threads, "kind": "port",
-                          "sample": f"T={p['T']} for {hv_s} of {p['Hv']} V-heads ({dt:.1f} s), scaled to all heads"}
-    # decode: 256 single-token steps over the full 16 x 32-head state
+                          "sample": f"{reps} x T={p['T']} for {hv_s} of {p['Hv']} V-heads ({dt:.1f} s)"}
+    # decode: 1024 single-token steps over the full 16 x 32-head state
     d = DECODE
-    steps = 256
+    steps = 1024
     qd, kd, vd = (dec[n].float().cpu().numpy()[:, None] for n in ("q", "k", "v"))
     bd, gd = (dec[n].cpu().numpy()[:, None] for n in ("beta", "g"))
     st = dec["states"][0].cpu().numpy()
@@ -262,6 +293,22 @@ def main():
     dec_rot_ms = e0.elapsed_time(e1) / n
     dec_res_ms = e2.elapsed_time(e3) / n
 
+    # gated GQA layer (outside the step): warm-up launch, then timed launches
+    gq = a["gqa"]
+
+    def gqa():
+        tsa.attn_gqa_fwd(gq["q"], gq["k"], gq["v"], gq["gate"], gq["o"], causal=True, stream=stream)
+
+    gqa()
+    n_gqa = max(3, min(K, 10))
+    e4, e5 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e4.record(stream)
+    for _ in range(n_gqa):
+        gqa()
+    e5.record(stream)
+    torch.cuda.synchronize()
+    gqa_ms = e4.elapsed_time(e5) / n_gqa
+
     if args.copy_calibration_mib > 0:
         n_el = args.copy_calibration_mib * (1 << 20) // 4
         src = torch.ones(n_el, dtype=torch.float32, device=dev)
@@ -272,7 +319,8 @@ def main():
         del src, dst
 
     finite = bool(torch.isfinite(a["o"]).all() and torch.isfinite(pre["out"]).all()
-                  and torch.isfinite(pre["state"]).all() and torch.isfinite(dec["out"]).all())
+                  and torch.isfinite(pre["state"]).all() and torch.isfinite(dec["out"]).all()
+                  and torch.isfinite(gq["o"]).all())
 
     traffic = load_traffic()
     fa = attn_flops(**ATTN)
@@ -280,6 +328,8 @@ def main():
     bp = prefill_bytes(**PREFILL)
     bd = decode_bytes(**DECODE)
     attn_tflops = fa / (ms["attn_fwd"] * 1e-3) / 1e12
+    fg = attn_flops(GQA["B"], GQA["Hq"], GQA["S"], GQA["D"], True)
+    gqa_tflops = fg / (gqa_ms * 1e-3) / 1e12
     pre_tflops = fp / (ms["gdn_prefill"] * 1e-3) / 1e12
     dec_gbs = bd / (ms["gdn_decode"] * 1e-3) / 1e9
 
@@ -301,6 +351,13 @@ def main():
             "bytes_per_launch": bp,
             "roofline": roof("mfma", pre_tflops, PEAK_MFMA_F16_TFLOPS, "TFLOP/s", "gdn_prefill"),
             "hbm_frac": round(bp / (ms["gdn_prefill"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        },
+        "attn_gqa_gated": {
+            "workload": "gated GQA attention fwd B=1 Hq=24 Hkv=4 S=8192 D=256 causal fp16, "
+                        "N(0,0.5), gate N(0,1); timed outside the step",
+            "value": round(gqa_tflops, 2), "unit": "TFLOP/s", "ms": round(gqa_ms, 5),
+            "flop_per_launch": fg,
+            "roofline": roof("mfma", gqa_tflops, PEAK_MFMA_F16_TFLOPS, "TFLOP/s", "attn_gqa_gated"),
         },
         "gdn_decode": {
             "workload": "GDN decode step, 16 sequences x 32 V-heads, 128x128 fp32 state, 16 replicas cycled back to back",
