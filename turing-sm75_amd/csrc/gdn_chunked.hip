@@ -295,8 +295,14 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
         for (int r = 0; r < 16; ++r) {
             const int t = 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
             sm.Wst[t * kD + cp] = (half_t)w_acc[n2][r];
-            sm.Ust[((((col >> 4) * 4 + (t >> 4)) * 64 + ((t >> 2) & 3) * 16 + (col & 15)) << 2) + (t & 3)] =
-                (half_t)u_acc[n2][r];
+        }
+        // U: registers 4a..4a+3 are tokens t0..t0+3 of one column, contiguous in the layout
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            const int t0 = 32 * mt + 8 * a + 4 * hi;
+            *reinterpret_cast<half4_t*>(&sm.Ust[(((col >> 4) * 4 + (t0 >> 4)) * 64 + ((t0 >> 2) & 3) * 16 + (col & 15)) << 2]) =
+                half4_t{(half_t)u_acc[n2][4 * a], (half_t)u_acc[n2][4 * a + 1], (half_t)u_acc[n2][4 * a + 2],
+                        (half_t)u_acc[n2][4 * a + 3]};
         }
     }
     lds_barrier();
