@@ -99,6 +99,42 @@ int tsa_gdn_decode_step(const void* q, const void* k, const void* v, const float
                         const float* beta, float* state, void* out, int B, int Hq, int Hv,
                         int dk, int dv, float scale, void* stream);
 
+/* ---- The Gated DeltaNet layer's pre / post ops (the target model's layer,
+ * docs/qwen38-27b.md:15).  The reference tree has no implementation of them: its inputs
+ * assume they were applied (q, k L2-normalised, beta and g_log given), as llama.cpp's graph
+ * does around gated_delta_net (the kernels' semantic source, src/gdn_sm75.cu:3).  Here:
+ *   q, k    <- x / max(||x||_2, eps) per [dk] row
+ *   g_log    = softplus(a + dt_bias[h]) * A[h]   (A = -exp(A_log); softplus passes x > 20)
+ *   beta     = sigmoid(b)
+ *   post:  y = x / sqrt(mean(x^2) + eps) * w * silu(z) per [dv] row
+ * a, b are fp32 [B][T][Hv], dt_bias and A fp32 [Hv], w fp32 [dv]; q/k/x/z/y fp16. ---- */
+
+/* The chunked prefill of tsa_gdn_chunked_fwd with the pre-ops fused: q, k are the raw rows
+ * and a, b the raw gate projections.  The norms fold into factors the prefill already
+ * applies, so the recurrence reads the raw rows with no extra pass.  Same workspace. */
+int tsa_gdn_chunked_fused_fwd(const void* q, const void* k, const void* v, const float* a,
+                              const float* b, const float* dt_bias, const float* A, float* state,
+                              void* out, int B, int T, int Hq, int Hv, int dk, int dv, int chunk,
+                              float scale, float eps, void* ws, size_t ws_bytes, void* stream);
+
+/* tsa_gdn_decode_step with the pre-ops fused (raw q, k rows; raw a, b [B][Hv]). */
+int tsa_gdn_decode_fused_step(const void* q, const void* k, const void* v, const float* a,
+                              const float* b, const float* dt_bias, const float* A, float* state,
+                              void* out, int B, int Hq, int Hv, int dk, int dv, float scale,
+                              float eps, void* stream);
+
+/* The pre-ops as their own pass (for tsa_gdn_recurrent_fwd and unfused callers): q_out,
+ * k_out fp16 [B][T][Hq][dk]; g_log, beta fp32 [B][T][Hv].  dk = 128. */
+int tsa_gdn_preprocess(const void* q, const void* k, const float* a, const float* b,
+                       const float* dt_bias, const float* A, void* q_out, void* k_out,
+                       float* g_log, float* beta, int B, int T, int Hq, int Hv, int dk,
+                       float eps, void* stream);
+
+/* The post-op: gated RMSNorm of the recurrence output x with the gate projection z, both
+ * fp16 [B][T][Hv][dv], weight w fp32 [dv], into y (may alias x).  dv = 128. */
+int tsa_gdn_gated_rmsnorm(const void* x, const void* z, const float* w, void* y, int B, int T,
+                          int Hv, int dv, float eps, void* stream);
+
 /* The lab's naive GDN check on the device: one thread per state column, fp32, state read
  * and written in global memory, the order of gdn_cpu (src/gdn_sm75.cu:1078-1106) and
  * gdn_serial_kernel (:57-92).  Used by the gdn driver's error check.  Any dk, dv >= 1. */

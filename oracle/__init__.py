@@ -189,3 +189,51 @@ def ref_solve(kb: np.ndarray) -> np.ndarray:
     out = np.empty(C * C, np.float32)
     load().orc_ref_solve(_ptr(kb.reshape(-1)), _ptr(out), C)
     return out
+
+
+# ---------------------------------------------------------------------------------------
+# GDN pre/post ops of the target model's Gated DeltaNet layer (docs/qwen38-27b.md:15; the
+# kernel's semantic source is llama.cpp's gated_delta_net, gdn_sm75.cu:3).  The reference
+# tree holds no implementation of them: these restate the published definitions in float64
+# (ggml's l2_norm, sigmoid, softplus and rms_norm, and the layer's gate g = softplus(a +
+# dt_bias) * A with A = -exp(A_log)).  Parity against ggml itself is unpinned; the tests
+# pin them by closed forms and invariants.
+# ---------------------------------------------------------------------------------------
+def l2norm_rows(x, eps: float = 1e-6) -> np.ndarray:
+    """x / max(||x||_2, eps) over the last axis, float64 (ggml_l2_norm's definition)."""
+    x = np.asarray(x, dtype=np.float64)
+    n = np.sqrt(np.sum(x * x, axis=-1, keepdims=True))
+    return x / np.maximum(n, eps)
+
+
+def softplus(x) -> np.ndarray:
+    """log(1 + e^x), float64; x above 20 passes through (the threshold ggml and torch use)."""
+    x = np.asarray(x, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+
+
+def sigmoid(x) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return 1.0 / (1.0 + np.exp(-x))
+
+
+def gdn_gates(a, b, dt_bias, A):
+    """(g_log, beta) from the layer's projections: a, b [..., Hv]; dt_bias, A [Hv]."""
+    g = softplus(np.asarray(a, np.float64) + np.asarray(dt_bias, np.float64)) * np.asarray(A, np.float64)
+    return g, sigmoid(b)
+
+
+def gdn_preprocess(q, k, a, b, dt_bias, A, eps: float = 1e-6):
+    """The pre-ops: l2-normalised q, k (float64) and g_log, beta (float64)."""
+    g, beta = gdn_gates(a, b, dt_bias, A)
+    return l2norm_rows(q, eps), l2norm_rows(k, eps), g, beta
+
+
+def gated_rmsnorm(x, z, w, eps: float = 1e-6) -> np.ndarray:
+    """The post-op: x / sqrt(mean(x^2) + eps) * w * silu(z) over the last axis, float64."""
+    x = np.asarray(x, dtype=np.float64)
+    z = np.asarray(z, dtype=np.float64)
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return x * r * np.asarray(w, np.float64) * (z * sigmoid(z))

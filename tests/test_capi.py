@@ -121,3 +121,38 @@ def test_drivers_usage_errors_exit_2(argv):
     assert os.path.exists(exe), "build the drivers first (make -C turing-sm75_amd)"
     r = subprocess.run([exe] + argv[1:], capture_output=True, text=True, timeout=60)
     assert r.returncode == 2, (r.returncode, r.stdout, r.stderr)
+
+
+def test_gdn_fused_and_op_argument_errors():
+    lib = tsa.load()
+    inf, nan = float("inf"), float("nan")
+    # chunked fused: q k v a b dt A state out | B T Hq Hv dk dv chunk | scale eps | ws ws_bytes stream
+    def fused(*, A=DUMMY, dk=128, chunk=64, eps=1e-6, ws=DUMMY, ws_bytes=1 << 30, T=64):
+        return lib.tsa_gdn_chunked_fused_fwd(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, A, DUMMY,
+                                             DUMMY, 1, T, 1, 2, dk, 128, chunk, 0.1, eps, ws,
+                                             ws_bytes, NULL)
+    assert fused(A=NULL) == tsa.TSA_ERR_NULL
+    assert fused(eps=0.0) == tsa.TSA_ERR_ARG
+    assert fused(eps=nan) == tsa.TSA_ERR_ARG
+    assert fused(dk=64) == tsa.TSA_ERR_UNSUPPORTED
+    assert fused(chunk=32) == tsa.TSA_ERR_UNSUPPORTED
+    assert fused(T=0) == tsa.TSA_ERR_SHAPE
+    assert fused(ws=NULL) == tsa.TSA_ERR_WORKSPACE
+    # decode fused: q k v a b dt A state out | B Hq Hv dk dv | scale eps | stream
+    args = [DUMMY] * 9
+    assert lib.tsa_gdn_decode_fused_step(*args, 4, 1, 2, 128, 128, 0.1, -1.0, NULL) == tsa.TSA_ERR_ARG
+    assert lib.tsa_gdn_decode_fused_step(*args, 4, 1, 2, 128, 128, inf, 1e-6, NULL) == tsa.TSA_ERR_ARG
+    assert lib.tsa_gdn_decode_fused_step(*args, 4, 1, 2, 96, 128, 0.1, 1e-6, NULL) == tsa.TSA_ERR_UNSUPPORTED
+    assert lib.tsa_gdn_decode_fused_step(*args[:5], NULL, *args[6:], 4, 1, 2, 128, 128, 0.1, 1e-6,
+                                         NULL) == tsa.TSA_ERR_NULL
+    # preprocess: q k a b dt A q_out k_out g beta | B T Hq Hv dk | eps | stream
+    pa = [DUMMY] * 10
+    assert lib.tsa_gdn_preprocess(*pa[:9], NULL, 1, 8, 2, 4, 128, 1e-6, NULL) == tsa.TSA_ERR_NULL
+    assert lib.tsa_gdn_preprocess(*pa, 1, 8, 2, 4, 64, 1e-6, NULL) == tsa.TSA_ERR_UNSUPPORTED
+    assert lib.tsa_gdn_preprocess(*pa, 1, 0, 2, 4, 128, 1e-6, NULL) == tsa.TSA_ERR_SHAPE
+    assert lib.tsa_gdn_preprocess(*pa, 1, 8, 2, 4, 128, 0.0, NULL) == tsa.TSA_ERR_ARG
+    # gated rmsnorm: x z w y | B T Hv dv | eps | stream
+    assert lib.tsa_gdn_gated_rmsnorm(DUMMY, NULL, DUMMY, DUMMY, 1, 2, 3, 128, 1e-6, NULL) == tsa.TSA_ERR_NULL
+    assert lib.tsa_gdn_gated_rmsnorm(DUMMY, DUMMY, DUMMY, DUMMY, 1, 2, 3, 64, 1e-6, NULL) == tsa.TSA_ERR_UNSUPPORTED
+    assert lib.tsa_gdn_gated_rmsnorm(DUMMY, DUMMY, DUMMY, DUMMY, 1, 0, 3, 128, 1e-6, NULL) == tsa.TSA_ERR_SHAPE
+    assert lib.tsa_gdn_gated_rmsnorm(DUMMY, DUMMY, DUMMY, DUMMY, 1, 2, 3, 128, inf, NULL) == tsa.TSA_ERR_ARG

@@ -46,6 +46,13 @@ int check_gdn(const void* q, const void* k, const void* v, const float* g, const
     return TSA_OK;
 }
 
+// The raw gate inputs of the fused pre-ops and the l2-norm eps.
+int check_gates(const float* a, const float* b, const float* dt_bias, const float* A, float eps) {
+    if (!a || !b || !dt_bias || !A) return TSA_ERR_NULL;
+    if (!(eps > 0.f) || !std::isfinite(eps)) return TSA_ERR_ARG;
+    return TSA_OK;
+}
+
 }  // namespace
 
 extern "C" const char* tsa_strerror(int code) {
@@ -56,7 +63,7 @@ extern "C" const char* tsa_strerror(int code) {
         case TSA_ERR_UNSUPPORTED: return "shape not supported by this build (attention: D in {64,128,256}; GDN: dk = dv = 128, chunk = 64)";
         case TSA_ERR_WORKSPACE: return "workspace is NULL or smaller than the required size";
         case TSA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
-        case TSA_ERR_ARG: return "invalid argument (causal not 0/1, or scale not finite / not > 0)";
+        case TSA_ERR_ARG: return "invalid argument (causal not 0/1, scale not finite / not > 0, or eps not finite / not > 0)";
         default: return "unknown tsa error code";
     }
 }
@@ -146,4 +153,62 @@ extern "C" int tsa_gdn_naive(const void* q, const void* k, const void* v, const 
     if (rc) return rc;
     return from_hip(tsa::gdn_naive(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv,
                                    scale, as_stream(stream)));
+}
+
+extern "C" int tsa_gdn_chunked_fused_fwd(const void* q, const void* k, const void* v, const float* a,
+                                         const float* b, const float* dt_bias, const float* A,
+                                         float* state, void* out, int B, int T, int Hq, int Hv,
+                                         int dk, int dv, int chunk, float scale, float eps, void* ws,
+                                         size_t ws_bytes, void* stream) {
+    int rc = check_gdn(q, k, v, a, b, state, out, B, T, Hq, Hv, dk, dv, scale);
+    if (rc) return rc;
+    rc = check_gates(a, b, dt_bias, A, eps);
+    if (rc) return rc;
+    if (chunk < 1) return TSA_ERR_SHAPE;
+    if (dk != 128 || dv != 128 || chunk != 64) return TSA_ERR_UNSUPPORTED;
+    const long long nch = (T + 63LL) / 64;
+    if (!fits_int(B, Hv, nch) || !fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
+    const size_t need = tsa::gdn_chunked_ws_bytes(B, T, Hv);
+    if (!ws || ws_bytes < need) return TSA_ERR_WORKSPACE;
+    return from_hip(tsa::gdn_chunked_fused(q, k, v, tsa::GdnRawGates{a, b, dt_bias, A, eps}, state,
+                                           out, B, T, Hq, Hv, scale, ws, as_stream(stream)));
+}
+
+extern "C" int tsa_gdn_decode_fused_step(const void* q, const void* k, const void* v, const float* a,
+                                         const float* b, const float* dt_bias, const float* A,
+                                         float* state, void* out, int B, int Hq, int Hv, int dk,
+                                         int dv, float scale, float eps, void* stream) {
+    int rc = check_gdn(q, k, v, a, b, state, out, B, 1, Hq, Hv, dk, dv, scale);
+    if (rc) return rc;
+    rc = check_gates(a, b, dt_bias, A, eps);
+    if (rc) return rc;
+    if (dk != 128 || dv != 128) return TSA_ERR_UNSUPPORTED;
+    if (!fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
+    return from_hip(tsa::gdn_decode_fused(q, k, v, tsa::GdnRawGates{a, b, dt_bias, A, eps}, state,
+                                          out, B, Hq, Hv, scale, as_stream(stream)));
+}
+
+extern "C" int tsa_gdn_preprocess(const void* q, const void* k, const float* a, const float* b,
+                                  const float* dt_bias, const float* A, void* q_out, void* k_out,
+                                  float* g_log, float* beta, int B, int T, int Hq, int Hv, int dk,
+                                  float eps, void* stream) {
+    if (!q || !k || !q_out || !k_out || !g_log || !beta) return TSA_ERR_NULL;
+    int rc = check_gates(a, b, dt_bias, A, eps);
+    if (rc) return rc;
+    if (B < 1 || T < 1 || Hq < 1 || Hv < 1 || dk < 1) return TSA_ERR_SHAPE;
+    if (dk != 128) return TSA_ERR_UNSUPPORTED;
+    // workgroups: 2 * B*T*Hq / 16 rows and B*T*Hv / 256 gates
+    if (!fits_int(B, T, Hq) || !fits_int(B, T, Hv)) return TSA_ERR_SHAPE;
+    return from_hip(tsa::gdn_preprocess(q, k, a, b, dt_bias, A, q_out, k_out, g_log, beta, B, T, Hq,
+                                        Hv, eps, as_stream(stream)));
+}
+
+extern "C" int tsa_gdn_gated_rmsnorm(const void* x, const void* z, const float* w, void* y, int B,
+                                     int T, int Hv, int dv, float eps, void* stream) {
+    if (!x || !z || !w || !y) return TSA_ERR_NULL;
+    if (B < 1 || T < 1 || Hv < 1 || dv < 1) return TSA_ERR_SHAPE;
+    if (dv != 128) return TSA_ERR_UNSUPPORTED;
+    if (!(eps > 0.f) || !std::isfinite(eps)) return TSA_ERR_ARG;
+    if (!fits_int(B, T, Hv)) return TSA_ERR_SHAPE;
+    return from_hip(tsa::gdn_gated_rmsnorm(x, z, w, y, B, T, Hv, eps, as_stream(stream)));
 }

@@ -60,6 +60,11 @@ __device__ __forceinline__ float sum8(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// The gates of the target model's Gated DeltaNet layer: softplus(x) = log(1 + e^x), with x
+// above 20 passed through (the threshold ggml and torch use), and the logistic sigmoid.
+__device__ __forceinline__ float gdn_softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float gdn_sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+
 // Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
 // outstanding global load and store of the wave (vmcnt counts both), which would drain
 // prefetches issued for later iterations; use this one where no global memory written

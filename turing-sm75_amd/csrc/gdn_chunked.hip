@@ -46,8 +46,10 @@ constexpr int kCarryThreads = 512;  // waves 0-1 chain, 2-3 output, 4-7 DMA
 constexpr int kWsW = 0;                     // fp16 [64 t][128]: column i stored at perm32(i)
 constexpr int kWsU = kWsW + kC * kD * 2;    // fp16 [8 strip][4 mtile][64 lane][4]
 constexpr int kWsAqk = kWsU + kC * kD * 2;  // fp16 [64 t][64]: column s stored at perm32(s)
-constexpr int kWsG = kWsAqk + kC * kC * 2;  // fp32 [64] e^{G_t}, then fp32 [64] e^{G_63 - G_t}
-constexpr int kWsChunk = kWsG + kC * 8;     // 41472 B, multiple of 256
+// fp32 [64] e^{G_t} qn_t, [64] e^{G_63 - G_t} kn_t, [64] {e^{G_63}, 0, ...}, [64] zeros, where
+// qn_t, kn_t are the l2-norm factors of the fused entry point's raw q / k rows (1 otherwise)
+constexpr int kWsG = kWsAqk + kC * kC * 2;
+constexpr int kWsChunk = kWsG + kC * 16;    // 41984 B, multiple of 256
 
 // Within each aligned 32-block, index 16a + 4g + b is stored at 8g + 4a + b.  A 16x16x32
 // MFMA lane of group g then finds its 8 k-values {16a + 4g + b} in one 16-byte run; that
@@ -102,13 +104,19 @@ struct PrepLds {
     float G[kC];
     float bt[kC];
     float bg[kC];
+    float kn[kC];  // l2-norm factors 1 / max(||k_t||, eps), 1 / max(||q_t||, eps) (fused only)
+    float qn[kC];
 };
 
+// kFused: q / k are the raw rows (normalised here: the factors scale A, Aqk, W and the
+// workspace's e^G / e^{G_63 - G}, so the carry multiplies raw K / Q rows by them for free),
+// and g_log / beta are computed from the raw projections a / b (gate arguments).
+template <bool kFused>
 __global__ void __launch_bounds__(kThreads, 3)
 gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
                const half_t* __restrict__ v, const float* __restrict__ g_log,
-               const float* __restrict__ beta, unsigned char* __restrict__ ws, int T, int Hq,
-               int Hv, int nch) {
+               const float* __restrict__ beta, GdnRawGates gates, unsigned char* __restrict__ ws,
+               int T, int Hq, int Hv, int nch) {
     __shared__ PrepLds sm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hi = lane >> 5;
     const int ch = blockIdx.x % nch;
@@ -133,6 +141,17 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
             vreg[it] = *reinterpret_cast<const uint4*>(v + (bt * Hv + h) * kD + c * 8);
         }
         *reinterpret_cast<uint4*>(sm.K + tile_off(r, c)) = kv;
+        if (kFused) {  // the row's 16 threads are 16 consecutive lanes of one wave
+            const half8_t k8 = __builtin_bit_cast(half8_t, kv);
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf((float)k8[e], (float)k8[e], ss);
+            ss += __shfl_xor(ss, 8);
+            ss += __shfl_xor(ss, 4);
+            ss += __shfl_xor(ss, 2);
+            ss += __shfl_xor(ss, 1);
+            if (c == 0) sm.kn[r] = 1.f / fmaxf(sqrtf(ss), gates.eps);
+        }
     }
     half8_t qa[kD / 16];
     {
@@ -141,23 +160,36 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
         for (int s = 0; s < kD / 16; ++s)
             qa[s] = tt < T ? *reinterpret_cast<const half8_t*>(qrow + 16 * s) : half8_t{};
+        if (kFused) {  // the two halves of the row are lanes l and l ^ 32
+            float ss = 0.f;
+#pragma unroll
+            for (int s = 0; s < kD / 16; ++s)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss = fmaf((float)qa[s][e], (float)qa[s][e], ss);
+            ss += __shfl_xor(ss, 32);
+            if (nt == 0 && hi == 0) sm.qn[32 * mt + (lane & 31)] = 1.f / fmaxf(sqrtf(ss), gates.eps);
+        }
     }
     if (wave == 0) {
         const int tt = t0 + lane;
         const size_t bt = (size_t)b * T + tt;
-        float x = tt < T ? g_log[bt * Hv + h] : 0.f;
-        const float be = tt < T ? beta[bt * Hv + h] : 0.f;
+        float x = 0.f, be = 0.f;
+        if (tt < T) {
+            if (kFused) {
+                x = gdn_softplus(gates.a[bt * Hv + h] + gates.dt_bias[h]) * gates.A[h];
+                be = gdn_sigmoid(gates.b[bt * Hv + h]);
+            } else {
+                x = g_log[bt * Hv + h];
+                be = beta[bt * Hv + h];
+            }
+        }
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {  // inclusive prefix sum over the chunk
             const float y = __shfl_up(x, off);
             if (lane >= off) x += y;
         }
-        const float ex = __expf(x);
         sm.G[lane] = x;
         sm.bt[lane] = be;
-        sm.bg[lane] = be * ex;
-        reinterpret_cast<float*>(wsc + kWsG)[lane] = ex;
-        reinterpret_cast<float*>(wsc + kWsG)[kC + lane] = __expf(__shfl(x, kC - 1) - x);
     }
     lds_barrier();
 
@@ -181,23 +213,41 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
             qk = mfma32(qa[s], bk, qk);
         }
         const float Gs = sm.G[rb];
+        const float kns = kFused ? sm.kn[rb] : 1.f;
         const int sp = perm32(rb);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int t = 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
             const float dec = (rb <= t) ? __expf(sm.G[t] - Gs) : 0.f;
-            if (rb < t) sm.A[t][rb] = sm.bt[t] * kk[r] * dec;
-            sm.Aqk[t * kC + sp] = (half_t)(qk[r] * dec);
+            if (kFused) {
+                if (rb < t) sm.A[t][rb] = sm.bt[t] * kk[r] * (dec * sm.kn[t] * kns);
+                sm.Aqk[t * kC + sp] = (half_t)(qk[r] * (dec * sm.qn[t] * kns));
+            } else {
+                if (rb < t) sm.A[t][rb] = sm.bt[t] * kk[r] * dec;
+                sm.Aqk[t * kC + sp] = (half_t)(qk[r] * dec);
+            }
         }
     }
     lds_barrier();
 
-    // ---- 3. Aqk out (its staging shares LDS with Tm); Tm = (I + A)^-1 ----
+    // ---- 3. Aqk out (its staging shares LDS with Tm); wave 1: the decay block and the W
+    // column scale beta e^G (kn); Tm = (I + A)^-1 ----
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int id = it * kThreads + tid;
         *reinterpret_cast<uint4*>(wsc + kWsAqk + (size_t)id * 16) =
             *reinterpret_cast<const uint4*>(sm.Aqk + id * 8);
+    }
+    if (wave == 1) {
+        const float x = sm.G[lane], xc = sm.G[kC - 1];
+        const float ex = __expf(x);
+        const float kn = kFused ? sm.kn[lane] : 1.f, qn = kFused ? sm.qn[lane] : 1.f;
+        sm.bg[lane] = sm.bt[lane] * ex * kn;
+        float* wg = reinterpret_cast<float*>(wsc + kWsG);
+        wg[lane] = ex * qn;
+        wg[kC + lane] = __expf(xc - x) * kn;
+        wg[2 * kC + lane] = lane == 0 ? __expf(xc) : 0.f;
+        wg[3 * kC + lane] = 0.f;
     }
     lds_barrier();
     if (wave == 0) {  // the four 16x16 diagonal blocks, one column per lane
@@ -321,13 +371,14 @@ struct ChainSlot {                   // operands of the loop-carried part of one
     half_t K[kC * kD];               // K rows, swizzled (read transposed by the update)
     half_t W[kC * kD];               // W rows (perm32 columns), swizzled
     half_t U[kStrips * 4 * 64 * 4];  // this workgroup's two U strips, accumulator order
-    float E[kC];                     // e^{G_t}
-    float Dg[kC];                    // e^{G_63 - G_t}
+    float E[kC];                     // e^{G_t} qn_t (the output's factor; unused here)
+    float Dg[kC];                    // e^{G_63 - G_t} kn_t
+    float Ec[2 * kC];                // e^{G_63} (the chunk's decay), then zeros
 };
 struct OutSlot {                     // operands of the output of one chunk
     half_t Q[kC * kD];               // Q rows, swizzled
     half_t A[kC * kC];               // Aqk rows (perm32 columns), 8-chunk swizzle
-    float E[kC];                     // e^{G_t} (followed in the workspace by e^{G_63 - G_t})
+    float E[kC];                     // e^{G_t} qn_t (followed in the workspace by e^{G_63 - G_t} kn_t)
     float Dg[kC];
 };
 struct CarryLds {
@@ -347,13 +398,13 @@ typedef __attribute__((address_space(3))) void* lds_void_t;
 
 // Per-chunk copies into LDS: 62 one-KiB LDS-DMA instructions (global_load_lds_dwordx4,
 // lane l copies 16 bytes to M0 + 16*l).  Instruction n < 37 fills the chain slot at byte
-// 1024*n (K tile n < 16, W tile, U strips 32..35, E/Dg 36); n >= 37 fills the out slot at
+// 1024*n (K tile n < 16, W tile, U strips 32..35, decay block 36); n >= 37 fills the out slot at
 // byte 1024*(n-37) (Q tile, Aqk tile, E/Dg 61).  The structs' members are laid out in that
 // order so that the LDS offset is just 1024 * tile index.  The four DMA waves (4-7) take
 // n = w + 4j; each lane's source offset for its instructions is fixed for the whole loop
 // and computed once, so an instruction costs a scalar M0 write and the DMA itself.
 constexpr int kDmaN = 62, kDmaChain = 37, kDmaPerWave = 16;
-constexpr int kDmaEChain = 36, kDmaEOut = 61;  // 512-byte copies: lanes 0-31 only
+constexpr int kDmaEOut = 61;  // a 512-byte copy: lanes 0-31 only
 
 // Source byte offset of instruction n for this lane, from the instruction's base pointer:
 // the row base of the chunk's first token (K / Q tiles, rows at rowbytes apart, rows
@@ -371,7 +422,7 @@ __device__ __forceinline__ unsigned dma_src_off(int n, int lane, unsigned rowbyt
             return kWsW + (row * kD + cch * 8) * 2;
         }
         if (i < 36) return kWsU + pair * 4096 + (i - 32) * 1024 + lane * 16;  // own U strips
-        return kWsG + (lane & 31) * 16;
+        return kWsG + lane * 16;                     // the whole 1-KiB decay block
     }
     if (i < 24) {                                    // Aqk rows, 8-chunk swizzle
         const int P = (i - 16) * 64 + lane, row = P >> 3, cch = (P & 7) ^ ((row >> 1) & 7);
@@ -432,7 +483,7 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
                     o = dma_src_off(n, lane, rowbytes, pair, chainslot ? last_c : last_o);
                 const unsigned char* base = chainslot ? (rows ? kb : wc) : (rows ? qb : wo);
                 const unsigned lds = (chainslot ? slot_lds[pc] : slot_lds[2 + po]) + 1024u * i;
-                dma_issue(base, o, lds, n == kDmaEChain || n == kDmaEOut);
+                dma_issue(base, o, lds, n == kDmaEOut);
             }
         };
         if ((do_c && last_c < kC - 1) || (do_o && last_o < kC - 1))
@@ -494,7 +545,7 @@ __device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs
         u[mt] = *reinterpret_cast<const half4_t*>(cs.U + ((sl * 4 + mt) * 64 + lane) * 4);
         d4[mt] = *reinterpret_cast<const float4*>(cs.Dg + 16 * mt + 4 * g);
     }
-    const float eGC = cs.E[kC - 1];
+    const float eGC = cs.Ec[0];
     // K^T operands of the state update, read transposed
     half8_t aK[8][2];
 #pragma unroll
@@ -700,22 +751,39 @@ size_t gdn_chunked_ws_bytes(int B, int T, int Hv) {
     return (size_t)B * Hv * nch * kWsChunk;
 }
 
-hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,
-                       const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
-                       float scale, void* ws, hipStream_t stream) {
+namespace {
+template <bool kFused>
+hipError_t launch_chunked(const void* q, const void* k, const void* v, const float* g_log,
+                          const float* beta, const GdnRawGates& gates, float* state, void* out,
+                          int B, int T, int Hq, int Hv, float scale, void* ws, hipStream_t stream) {
     const int nch = (T + kC - 1) / kC;
     const int BHv = B * Hv;
     auto Q = static_cast<const half_t*>(q);
     auto K = static_cast<const half_t*>(k);
     auto W = static_cast<unsigned char*>(ws);
-    hipLaunchKernelGGL(gdn_chunk_prep, dim3(BHv * nch), dim3(kThreads), 0, stream, Q, K,
-                       static_cast<const half_t*>(v), g_log, beta, W, T, Hq, Hv, nch);
+    hipLaunchKernelGGL(gdn_chunk_prep<kFused>, dim3(BHv * nch), dim3(kThreads), 0, stream, Q, K,
+                       static_cast<const half_t*>(v), g_log, beta, gates, W, T, Hq, Hv, nch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(gdn_chunk_carry, dim3(BHv * (kD / (16 * kStrips))), dim3(kCarryThreads), 0,
                        stream, Q, K, W, state, static_cast<half_t*>(out), T, Hq, Hv, nch, BHv,
                        scale);
     return hipGetLastError();
+}
+}  // namespace
+
+hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,
+                       const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
+                       float scale, void* ws, hipStream_t stream) {
+    return launch_chunked<false>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq, Hv,
+                                 scale, ws, stream);
+}
+
+hipError_t gdn_chunked_fused(const void* q, const void* k, const void* v, const GdnRawGates& gates,
+                             float* state, void* out, int B, int T, int Hq, int Hv, float scale,
+                             void* ws, hipStream_t stream) {
+    return launch_chunked<true>(q, k, v, nullptr, nullptr, gates, state, out, B, T, Hq, Hv, scale,
+                                ws, stream);
 }
 
 }  // namespace tsa

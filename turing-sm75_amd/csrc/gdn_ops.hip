@@ -1,0 +1,114 @@
+// gdn_ops.hip -- the element-wise operations on either side of the Gated DeltaNet recurrence
+// in the target model's layer (docs/qwen38-27b.md:15; the recurrence's semantic source is
+// llama.cpp's gated_delta_net, src/gdn_sm75.cu:3):
+//   pre:  q, k <- x / max(||x||_2, eps) per head row;  beta = sigmoid(b);
+//         g_log = softplus(a + dt_bias[h]) * A[h]   (A = -exp(A_log), per V-head)
+//   post: y = x / sqrt(mean(x^2) + eps) * w * silu(z)   per (token, V-head) row
+// All are HBM-bound streams of 256-byte rows: a row belongs to 16 lanes that each move 16
+// bytes, so every instruction covers whole 128-byte lines, and the row sums are 4 lane
+// exchanges inside the 16-lane group.  The fused prefill / decode entry points apply the
+// pre-ops inside the recurrence kernels instead (gdn_chunked.hip, gdn_recurrent.hip).
+#include "common.h"
+#include "kernels.h"
+
+namespace tsa {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kRowsPerBlock = 16;  // 256 threads, 16 per row
+
+__device__ __forceinline__ float sum16(float x) {
+    x += __shfl_xor(x, 8);
+    x += __shfl_xor(x, 4);
+    x += __shfl_xor(x, 2);
+    x += __shfl_xor(x, 1);
+    return x;
+}
+
+// Rows [0, rows) of x0 and then rows [0, rows) of x1, normalised into y0 / y1.
+__global__ void __launch_bounds__(256)
+l2norm_rows_kernel(const half_t* x0, half_t* y0, const half_t* x1,  // y may alias x
+                   half_t* y1, long long rows, float eps) {
+    const long long r = (long long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
+    if (r >= 2 * rows) return;  // whole 16-lane groups leave together
+    const int c = threadIdx.x & 15;
+    const bool second = r >= rows;
+    const long long rr = second ? r - rows : r;
+    const half_t* x = (second ? x1 : x0) + rr * kD + 8 * c;
+    half_t* y = (second ? y1 : y0) + rr * kD + 8 * c;
+    const half8_t v = *reinterpret_cast<const half8_t*>(x);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf((float)v[e], (float)v[e], ss);
+    const float inv = 1.f / fmaxf(sqrtf(sum16(ss)), eps);
+    half8_t o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (half_t)((float)v[e] * inv);
+    *reinterpret_cast<half8_t*>(y) = o;
+}
+
+__global__ void __launch_bounds__(256)
+gdn_gates_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                 const float* __restrict__ dt_bias, const float* __restrict__ A,
+                 float* __restrict__ g_log, float* __restrict__ beta, long long n, int Hv) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int h = (int)(i % Hv);
+    g_log[i] = gdn_softplus(a[i] + dt_bias[h]) * A[h];
+    beta[i] = gdn_sigmoid(b[i]);
+}
+
+__global__ void __launch_bounds__(256)
+gated_rmsnorm_kernel(const half_t* x, const half_t* __restrict__ z,
+                     const float* __restrict__ w, half_t* y, long long rows, float eps) {  // y may alias x
+    const long long r = (long long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
+    if (r >= rows) return;
+    const int c = threadIdx.x & 15;
+    const half8_t xv = *reinterpret_cast<const half8_t*>(x + r * kD + 8 * c);
+    const half8_t zv = *reinterpret_cast<const half8_t*>(z + r * kD + 8 * c);
+    const float4 w0 = *reinterpret_cast<const float4*>(w + 8 * c);
+    const float4 w1 = *reinterpret_cast<const float4*>(w + 8 * c + 4);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf((float)xv[e], (float)xv[e], ss);
+    const float rs = 1.f / sqrtf(sum16(ss) * (1.f / kD) + eps);
+    half8_t o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float zf = (float)zv[e];
+        o[e] = (half_t)((float)xv[e] * rs * wv[e] * (zf * gdn_sigmoid(zf)));
+    }
+    *reinterpret_cast<half8_t*>(y + r * kD + 8 * c) = o;
+}
+
+}  // namespace
+
+hipError_t gdn_preprocess(const void* q, const void* k, const float* a, const float* b,
+                          const float* dt_bias, const float* A, void* q_out, void* k_out,
+                          float* g_log, float* beta, int B, int T, int Hq, int Hv, float eps,
+                          hipStream_t stream) {
+    const long long rows = (long long)B * T * Hq;
+    const long long nb = (2 * rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    hipLaunchKernelGGL(l2norm_rows_kernel, dim3((unsigned)nb), dim3(256), 0, stream,
+                       static_cast<const half_t*>(q), static_cast<half_t*>(q_out),
+                       static_cast<const half_t*>(k), static_cast<half_t*>(k_out), rows, eps);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const long long n = (long long)B * T * Hv;
+    hipLaunchKernelGGL(gdn_gates_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a,
+                       b, dt_bias, A, g_log, beta, n, Hv);
+    return hipGetLastError();
+}
+
+hipError_t gdn_gated_rmsnorm(const void* x, const void* z, const float* w, void* y, int B, int T,
+                             int Hv, float eps, hipStream_t stream) {
+    const long long rows = (long long)B * T * Hv;
+    const long long nb = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3((unsigned)nb), dim3(256), 0, stream,
+                       static_cast<const half_t*>(x), static_cast<const half_t*>(z), w,
+                       static_cast<half_t*>(y), rows, eps);
+    return hipGetLastError();
+}
+
+}  // namespace tsa

@@ -106,12 +106,14 @@ gdn_recurrent_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
 // column) come in through LDS: wave 0 loads them with one 8-byte load per lane instead of
 // every thread issuing eight.  Measured over 16 x 32 heads: 16 columns per workgroup
 // (4096 workgroups) beat 32 and 64, and walking several column blocks per workgroup with
-// the next block's state prefetched gained nothing.
-template <int kCols>
+// the next block's state prefetched gained nothing.  kFused: q / k are raw rows, normalised
+// here (their norms come from the same 8-lane sums as the dot products), and g_log / beta
+// come from the raw projections a / b (gate arguments).
+template <int kCols, bool kFused>
 __global__ void __launch_bounds__(8 * kCols)
 gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
                   const half_t* __restrict__ v, const float* __restrict__ g_log,
-                  const float* __restrict__ beta, float* __restrict__ state,
+                  const float* __restrict__ beta, GdnRawGates gates, float* __restrict__ state,
                   half_t* __restrict__ out, int Hq, int Hv, float scale) {
     constexpr int kWgPerHead = kD / kCols;
     const int bh = blockIdx.x / kWgPerHead;
@@ -131,8 +133,14 @@ gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
         kq_rows[tid >> 5][tid & 31] = *reinterpret_cast<const half4_t*>(row + 4 * (tid & 31));
     }
     const float vc = (float)v[vrow + col];
-    const float g = __expf(g_log[bt * Hv + h]);
-    const float be = beta[bt * Hv + h];
+    float g, be;
+    if (kFused) {
+        g = __expf(gdn_softplus(gates.a[bt * Hv + h] + gates.dt_bias[h]) * gates.A[h]);
+        be = gdn_sigmoid(gates.b[bt * Hv + h]);
+    } else {
+        g = __expf(g_log[bt * Hv + h]);
+        be = beta[bt * Hv + h];
+    }
     __syncthreads();
     float kr[16], qr[16];
 #pragma unroll
@@ -157,6 +165,21 @@ gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
     kv = sum8(kv);
     sq = sum8(sq);
     kq = sum8(kq);
+    if (kFused) {  // k -> k / max(||k||, eps), q likewise: scale the sums and k itself
+        float kk = 0.f, qq = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            kk = fmaf(kr[i], kr[i], kk);
+            qq = fmaf(qr[i], qr[i], qq);
+        }
+        const float kn = 1.f / fmaxf(sqrtf(sum8(kk)), gates.eps);
+        const float qn = 1.f / fmaxf(sqrtf(sum8(qq)), gates.eps);
+        kv *= kn;
+        sq *= qn;
+        kq *= kn * qn;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) kr[i] *= kn;
+    }
     const float d = (vc - g * kv) * be;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -207,9 +230,9 @@ hipError_t gdn_recurrent(const void* q, const void* k, const void* v, const floa
                          int Hv, float scale, hipStream_t stream) {
     if (T == 1) {
         const unsigned blocks = (unsigned)(B * Hv * (kD / kDecodeCols));
-        hipLaunchKernelGGL(gdn_decode_kernel<kDecodeCols>, dim3(blocks), dim3(8 * kDecodeCols), 0,
-                           stream, static_cast<const half_t*>(q), static_cast<const half_t*>(k),
-                           static_cast<const half_t*>(v), g_log, beta, state,
+        hipLaunchKernelGGL((gdn_decode_kernel<kDecodeCols, false>), dim3(blocks), dim3(8 * kDecodeCols),
+                           0, stream, static_cast<const half_t*>(q), static_cast<const half_t*>(k),
+                           static_cast<const half_t*>(v), g_log, beta, GdnRawGates{}, state,
                            static_cast<half_t*>(out), Hq, Hv, scale);
         return hipGetLastError();
     }
@@ -218,6 +241,17 @@ hipError_t gdn_recurrent(const void* q, const void* k, const void* v, const floa
                        static_cast<const half_t*>(q), static_cast<const half_t*>(k),
                        static_cast<const half_t*>(v), g_log, beta, state,
                        static_cast<half_t*>(out), T, Hq, Hv, scale);
+    return hipGetLastError();
+}
+
+hipError_t gdn_decode_fused(const void* q, const void* k, const void* v, const GdnRawGates& gates,
+                            float* state, void* out, int B, int Hq, int Hv, float scale,
+                            hipStream_t stream) {
+    const unsigned blocks = (unsigned)(B * Hv * (kD / kDecodeCols));
+    hipLaunchKernelGGL((gdn_decode_kernel<kDecodeCols, true>), dim3(blocks), dim3(8 * kDecodeCols), 0,
+                       stream, static_cast<const half_t*>(q), static_cast<const half_t*>(k),
+                       static_cast<const half_t*>(v), nullptr, nullptr, gates, state,
+                       static_cast<half_t*>(out), Hq, Hv, scale);
     return hipGetLastError();
 }
 

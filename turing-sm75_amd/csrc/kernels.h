@@ -13,6 +13,17 @@ hipError_t attn_naive(const void* q, const void* k, const void* v, const void* g
                       int B, int Hq, int Hkv, int S, int D, float scale, int causal,
                       hipStream_t stream);
 
+// Raw inputs of the fused pre-ops (the target model's layer): a, b [B][T][Hv]; dt_bias, A
+// [Hv] (A = -exp(A_log)); eps of the q / k l2 norms.  g_log = softplus(a + dt_bias) * A,
+// beta = sigmoid(b), q and k normalised per head row.
+struct GdnRawGates {
+    const float* a;
+    const float* b;
+    const float* dt_bias;
+    const float* A;
+    float eps;
+};
+
 size_t gdn_chunked_ws_bytes(int B, int T, int Hv);
 hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,
                        const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
@@ -20,6 +31,18 @@ hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float*
 hipError_t gdn_recurrent(const void* q, const void* k, const void* v, const float* g_log,
                          const float* beta, float* state, void* out, int B, int T, int Hq,
                          int Hv, float scale, hipStream_t stream);
+hipError_t gdn_chunked_fused(const void* q, const void* k, const void* v, const GdnRawGates& gates,
+                             float* state, void* out, int B, int T, int Hq, int Hv, float scale,
+                             void* ws, hipStream_t stream);
+hipError_t gdn_decode_fused(const void* q, const void* k, const void* v, const GdnRawGates& gates,
+                            float* state, void* out, int B, int Hq, int Hv, float scale,
+                            hipStream_t stream);
+hipError_t gdn_preprocess(const void* q, const void* k, const float* a, const float* b,
+                          const float* dt_bias, const float* A, void* q_out, void* k_out,
+                          float* g_log, float* beta, int B, int T, int Hq, int Hv, float eps,
+                          hipStream_t stream);
+hipError_t gdn_gated_rmsnorm(const void* x, const void* z, const float* w, void* y, int B, int T,
+                             int Hv, float eps, hipStream_t stream);
 hipError_t gdn_naive(const void* q, const void* k, const void* v, const float* g_log,
                      const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
                      int dk, int dv, float scale, hipStream_t stream);

@@ -45,6 +45,10 @@ _SIGNATURES = {
     "tsa_gdn_recurrent_fwd": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
     "tsa_gdn_decode_step": (_i, [_vp] * 7 + [_i] * 5 + [_f, _vp]),
     "tsa_gdn_naive": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
+    "tsa_gdn_chunked_fused_fwd": (_i, [_vp] * 9 + [_i] * 7 + [_f, _f, _vp, _sz, _vp]),
+    "tsa_gdn_decode_fused_step": (_i, [_vp] * 9 + [_i] * 5 + [_f, _f, _vp]),
+    "tsa_gdn_preprocess": (_i, [_vp] * 10 + [_i] * 5 + [_f, _vp]),
+    "tsa_gdn_gated_rmsnorm": (_i, [_vp] * 4 + [_i] * 4 + [_f, _vp]),
 }
 
 
@@ -250,3 +254,91 @@ def gdn_decode_step(q, k, v, g_log, beta, state, out=None, scale=None, stream=No
 def gdn_naive(q, k, v, g_log, beta, state, out=None, scale=None, stream=None):
     """The naive on-device check kernel (one thread per state column)."""
     return gdn_recurrent_fwd(q, k, v, g_log, beta, state, out, scale, stream, naive=True)
+
+
+# ---- the layer's pre / post ops (q, k l2 norm; beta = sigmoid(b); g_log = softplus(a +
+# dt_bias) * A; gated RMSNorm of the output), fused or as passes of their own ----
+def _gates(a, b, dt_bias, A, lead, Hv):
+    import torch
+    for name, t in (("a", a), ("b", b)):
+        _need(t, torch.float32, len(lead) + 1, name)
+        if tuple(t.shape) != tuple(lead) + (Hv,):
+            raise ValueError(f"{name}: expected shape {tuple(lead) + (Hv,)}, got {tuple(t.shape)}")
+    for name, t in (("dt_bias", dt_bias), ("A", A)):
+        _need(t, torch.float32, 1, name)
+        if t.numel() != Hv:
+            raise ValueError(f"{name}: expected {Hv} values, got {t.numel()}")
+
+
+def gdn_chunked_fused_fwd(q, k, v, a, b, dt_bias, A, state, out=None, scale=None, eps=1e-6,
+                          chunk=64, ws=None, stream=None):
+    """Chunked prefill from raw q, k [B,T,Hq,dk] and raw gate projections a, b [B,T,Hv]."""
+    import torch
+    B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, a, b, state, True)
+    _gates(a, b, dt_bias, A, (B, T), Hv)
+    if out is None:
+        out = torch.empty_like(v)
+    _need(out, torch.float16, 4, "out")
+    if scale is None:
+        scale = 1.0 / math.sqrt(dk)
+    need = gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk)
+    if ws is None:
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    _check(load().tsa_gdn_chunked_fused_fwd(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b), _ptr(dt_bias), _ptr(A), _ptr(state),
+        _ptr(out), B, T, Hq, Hv, dk, dv, chunk, float(scale), float(eps), _ptr(ws),
+        ws.numel() * ws.element_size(), _stream(stream)))
+    return out
+
+
+def gdn_decode_fused_step(q, k, v, a, b, dt_bias, A, state, out=None, scale=None, eps=1e-6,
+                          stream=None):
+    """One decode step from raw q, k [B,Hq,dk] and raw gate projections a, b [B,Hv]."""
+    import torch
+    B, _, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, a, b, state, False)
+    _gates(a, b, dt_bias, A, (B,), Hv)
+    if out is None:
+        out = torch.empty_like(v)
+    _need(out, torch.float16, 3, "out")
+    if scale is None:
+        scale = 1.0 / math.sqrt(dk)
+    _check(load().tsa_gdn_decode_fused_step(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b), _ptr(dt_bias), _ptr(A), _ptr(state),
+        _ptr(out), B, Hq, Hv, dk, dv, float(scale), float(eps), _stream(stream)))
+    return out
+
+
+def gdn_preprocess(q, k, a, b, dt_bias, A, eps=1e-6, stream=None):
+    """The pre-ops as a pass: returns (q_n, k_n, g_log, beta) for raw q, k [B,T,Hq,dk]."""
+    import torch
+    _need(q, torch.float16, 4, "q")
+    _need(k, torch.float16, 4, "k")
+    if k.shape != q.shape:
+        raise ValueError("q and k must have the same shape")
+    B, T, Hq, dk = q.shape
+    Hv = a.shape[-1]
+    _gates(a, b, dt_bias, A, (B, T), Hv)
+    qn, kn = torch.empty_like(q), torch.empty_like(k)
+    g_log, beta = torch.empty_like(a), torch.empty_like(b)
+    _check(load().tsa_gdn_preprocess(
+        _ptr(q), _ptr(k), _ptr(a), _ptr(b), _ptr(dt_bias), _ptr(A), _ptr(qn), _ptr(kn),
+        _ptr(g_log), _ptr(beta), B, T, Hq, Hv, dk, float(eps), _stream(stream)))
+    return qn, kn, g_log, beta
+
+
+def gdn_gated_rmsnorm(x, z, w, out=None, eps=1e-6, stream=None):
+    """y = x / sqrt(mean(x^2) + eps) * w * silu(z) over dv; x, z [B,T,Hv,dv] fp16, w [dv]."""
+    import torch
+    _need(x, torch.float16, 4, "x")
+    _need(z, torch.float16, 4, "z")
+    _need(w, torch.float32, 1, "w")
+    if z.shape != x.shape or w.numel() != x.shape[3]:
+        raise ValueError("inconsistent shapes: x %s z %s w %s" % (tuple(x.shape), tuple(z.shape),
+                                                                 tuple(w.shape)))
+    if out is None:
+        out = torch.empty_like(x)
+    _need(out, torch.float16, 4, "out")
+    B, T, Hv, dv = x.shape
+    _check(load().tsa_gdn_gated_rmsnorm(_ptr(x), _ptr(z), _ptr(w), _ptr(out), B, T, Hv, dv,
+                                        float(eps), _stream(stream)))
+    return out
