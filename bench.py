@@ -18,7 +18,10 @@ W untimed warmup steps, then exactly K timed steps between two synchronisations.
 kernel's average duration comes from HIP events recorded on the stream it runs on.
 After the timed steps, outside the step, the gated grouped-query attention layer of the
 reference's target model (B=1, 24 query / 4 K/V heads, D=256, S=8192, causal, gate after
-softmax) is timed on its own and reported as the part `attn_gqa_gated`.
+softmax) is timed on its own and reported as the part `attn_gqa_gated`; so is the GDN
+recurrence with the layer's pre/post ops at the prefill shape (`gdn_layer_ops`): raw q/k
+and gate projections -> fused chunked prefill -> gated RMSNorm, against the unfused
+pipeline (pre-op pass, chunked prefill, gated RMSNorm).
 
 Printed: one JSON line.  `value` is the attention forward throughput (TFLOP/s, causal
 executed FLOPs 2*B*H*S*(S+1)*D, the convention of src/attn_sm75.cu:534), the kernel that
@@ -65,6 +68,11 @@ def prefill_flops(B, T, Hq, Hv, d, chunk, **_):
 def prefill_bytes(B, T, Hq, Hv, d, **_):
     return float(2 * B * T * Hq * d * 2 + 2 * B * T * Hv * d * 2 + 2 * B * T * Hv * 4
                  + 2 * B * Hv * d * d * 4)
+
+
+def rmsnorm_bytes(B, T, Hv, d, **_):
+    """Gated RMSNorm: read x and z, write y (fp16 rows of d), plus the fp32 weight."""
+    return 3 * B * T * Hv * d * 2 + d * 4
 
 
 def decode_bytes(B, Hq, Hv, d, **_):
@@ -138,7 +146,24 @@ def make_inputs(torch, dev, seed=2026):
     return a, pre, dec
 
 
-def cpu_baselines(torch, a, pre, dec, threads):
+def layer_inputs(torch, dev, pre):
+    """Raw inputs of the GDN layer at the prefill shape: q, k rows before the l2 norm, the
+    gate projections a, b, dt_bias, A = -exp(A_log), the output gate z and norm weight w."""
+    p = PREFILL
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    B, T, Hq, Hv, d = p["B"], p["T"], p["Hq"], p["Hv"], p["d"]
+    r = lambda *shape: torch.randn(*shape, device=dev, generator=gen)
+    lay = dict(q=r(B, T, Hq, d).half(), k=r(B, T, Hq, d).half(), a=r(B, T, Hv), b=r(B, T, Hv),
+               dt=0.5 * r(Hv), A=-torch.exp(0.5 * r(Hv)), z=r(B, T, Hv, d).half(),
+               w=1 + 0.1 * r(d))
+    lay["state"] = torch.zeros(B, Hv, d, d, device=dev)
+    lay["o"] = torch.empty(B, T, Hv, d, device=dev, dtype=torch.float16)
+    lay["y"] = torch.empty_like(lay["o"])
+    return lay
+
+
+def cpu_baselines(torch, a, pre, dec, threads, lay=None):
     """Time the oracle (the reference's naive paths restated in C++) on bounded samples."""
     import numpy as np
     import oracle
@@ -183,6 +208,19 @@ def cpu_baselines(torch, a, pre, dec, threads):
     tok_s = reps * p["B"] * p["T"] / (dt * p["Hv"] / hv_s)
     res["gdn_prefill"] = {"value": tok_s, "unit": "tok/s", "cores": threads, "kind": "port",
                           "sample": f"{reps} x T={p['T']} for {hv_s} of {p['Hv']} V-heads ({dt:.1f} s)"}
+    # GDN layer ops: the pre-ops, the serial recurrence and the gated RMSNorm on all heads
+    if lay is not None:
+        ln = lambda n: lay[n].float().cpu().numpy()
+        t0 = time.perf_counter()
+        qn, kn, gg, bb = oracle.gdn_preprocess(ln("q"), ln("k"), ln("a"), ln("b"), ln("dt"), ln("A"))
+        o, _ = oracle.gdn_serial(qn, kn, pre["v"].float().cpu().numpy(), gg, bb,
+                                 np.zeros((1, p["Hv"], p["d"], p["d"]), np.float32), nthreads=threads)
+        oracle.gated_rmsnorm(o, ln("z"), ln("w"))
+        dt = time.perf_counter() - t0
+        res["gdn_layer_ops"] = {"value": p["B"] * p["T"] / dt, "unit": "tok/s", "cores": threads,
+                                "kind": "port",
+                                "sample": f"T={p['T']} x {p['Hv']} V-heads, pre-ops + serial recurrence "
+                                          f"+ gated RMSNorm ({dt:.1f} s)"}
     # decode: 1024 single-token steps over the full 16 x 32-head state
     d = DECODE
     steps = 1024
@@ -309,6 +347,40 @@ def main():
     torch.cuda.synchronize()
     gqa_ms = e4.elapsed_time(e5) / n_gqa
 
+    # GDN layer ops at the prefill shape (outside the step): fused vs unfused pipelines
+    lay = layer_inputs(torch, dev, pre)
+
+    def fused_layer():
+        lay["state"].zero_()
+        tsa.gdn_chunked_fused_fwd(lay["q"], lay["k"], pre["v"], lay["a"], lay["b"], lay["dt"],
+                                  lay["A"], lay["state"], lay["o"], ws=ws, stream=stream)
+        tsa.gdn_gated_rmsnorm(lay["o"], lay["z"], lay["w"], out=lay["y"], stream=stream)
+
+    def unfused_layer():
+        lay["state"].zero_()
+        qn, kn, gl, be = tsa.gdn_preprocess(lay["q"], lay["k"], lay["a"], lay["b"], lay["dt"],
+                                            lay["A"], stream=stream)
+        tsa.gdn_chunked_fwd(qn, kn, pre["v"], gl, be, lay["state"], lay["o"], ws=ws, stream=stream)
+        tsa.gdn_gated_rmsnorm(lay["o"], lay["z"], lay["w"], out=lay["y"], stream=stream)
+
+    def rms_only():
+        tsa.gdn_gated_rmsnorm(lay["o"], lay["z"], lay["w"], out=lay["y"], stream=stream)
+
+    def time_fn(fn, n):
+        fn()
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record(stream)
+        for _ in range(n):
+            fn()
+        a1.record(stream)
+        torch.cuda.synchronize()
+        return a0.elapsed_time(a1) / n
+
+    n_lay = max(5, min(K, 20))
+    fused_ms = time_fn(fused_layer, n_lay)
+    unfused_ms = time_fn(unfused_layer, n_lay)
+    rms_ms = time_fn(rms_only, n_lay)
+
     if args.copy_calibration_mib > 0:
         n_el = args.copy_calibration_mib * (1 << 20) // 4
         src = torch.ones(n_el, dtype=torch.float32, device=dev)
@@ -320,7 +392,7 @@ def main():
 
     finite = bool(torch.isfinite(a["o"]).all() and torch.isfinite(pre["out"]).all()
                   and torch.isfinite(pre["state"]).all() and torch.isfinite(dec["out"]).all()
-                  and torch.isfinite(gq["o"]).all())
+                  and torch.isfinite(gq["o"]).all() and torch.isfinite(lay["y"]).all())
 
     traffic = load_traffic()
     fa = attn_flops(**ATTN)
@@ -359,6 +431,17 @@ def main():
             "flop_per_launch": fg,
             "roofline": roof("mfma", gqa_tflops, PEAK_MFMA_F16_TFLOPS, "TFLOP/s", "attn_gqa_gated"),
         },
+        "gdn_layer_ops": {
+            "workload": "GDN layer at the prefill shape from raw inputs (q/k rows N(0,1), gate "
+                        "projections a, b): fused pre-ops + chunked prefill + gated RMSNorm; "
+                        "timed outside the step",
+            "value": round(PREFILL["B"] * PREFILL["T"] / (fused_ms * 1e-3), 1), "unit": "tok/s",
+            "ms_fused": round(fused_ms, 5), "ms_unfused": round(unfused_ms, 5),
+            "ms_gated_rmsnorm": round(rms_ms, 5),
+            "gated_rmsnorm_bytes": rmsnorm_bytes(**PREFILL),
+            "roofline": roof("hbm", rmsnorm_bytes(**PREFILL) / (rms_ms * 1e-3) / 1e9, PEAK_HBM_GBS,
+                             "GB/s", "gdn_gated_rmsnorm"),
+        },
         "gdn_decode": {
             "workload": "GDN decode step, 16 sequences x 32 V-heads, 128x128 fp32 state, 16 replicas cycled back to back",
             "value": round(dec_gbs, 1), "unit": "GB/s", "ms": round(ms["gdn_decode"], 5),
@@ -373,7 +456,7 @@ def main():
     }
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baselines(torch, a, pre, dec, omp_threads())
+        cpu = cpu_baselines(torch, a, pre, dec, omp_threads(), lay)
         for k, v in cpu.items():
             out_parts[k]["cpu_baseline"] = {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                                             for kk, vv in v.items()}
