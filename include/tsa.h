@@ -22,6 +22,7 @@
 #ifndef TSA_H
 #define TSA_H
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -134,6 +135,33 @@ int tsa_gdn_preprocess(const void* q, const void* k, const float* a, const float
  * fp16 [B][T][Hv][dv], weight w fp32 [dv], into y (may alias x).  dv = 128. */
 int tsa_gdn_gated_rmsnorm(const void* x, const void* z, const float* w, void* y, int B, int T,
                           int Hv, int dv, float eps, void* stream);
+
+/* ---- ggml-layout adapter (the reference's kernels stand in for llama.cpp's
+ * gated_delta_net, src/gdn_sm75.cu:3, docs/ggml-turing.md:15-17; ggml is not vendored, so
+ * parity with ggml's own op is unpinned).  A tsa_tensor carries the fields of a
+ * ggml_tensor view: ne[0] is the innermost dimension, nb[] are byte strides. ---- */
+enum { TSA_TYPE_F32 = 0, TSA_TYPE_F16 = 1 }; /* ggml's GGML_TYPE_F32 / GGML_TYPE_F16 */
+typedef struct tsa_tensor {
+    void* data;
+    int type;
+    int64_t ne[4];
+    size_t nb[4];
+} tsa_tensor;
+
+/* Scratch the adapter needs for these shapes (q: [S, Hk, T, B], v: [S, Hv, T, B]); 0 if
+ * the shapes are invalid or unsupported. */
+size_t tsa_ggml_gdn_workspace_bytes(const tsa_tensor* q, const tsa_tensor* v);
+
+/* The recurrence on ggml views: q, k [S, Hk, T, B]; v, out [S, Hv, T, B] (fp32 or fp16,
+ * any strides); g_log, beta [Hv, T, B, 1] and state, state_out [S, S, Hv, B] fp32
+ * (state_out may be state itself, the same view).  S = 128; V-head h reads QK head h % Hk.
+ * Dispatches on T: the decode step (T = 1), the token-serial kernel, or the chunked
+ * prefill.  Dense fp16 / fp32 operands are used in place; others are gathered into ws. */
+int tsa_ggml_gated_delta_net(const tsa_tensor* q, const tsa_tensor* k, const tsa_tensor* v,
+                             const tsa_tensor* g_log, const tsa_tensor* beta,
+                             const tsa_tensor* state, const tsa_tensor* out,
+                             const tsa_tensor* state_out, float scale, void* ws,
+                             size_t ws_bytes, void* stream);
 
 /* The lab's naive GDN check on the device: one thread per state column, fp32, state read
  * and written in global memory, the order of gdn_cpu (src/gdn_sm75.cu:1078-1106) and

@@ -156,3 +156,62 @@ def test_gdn_fused_and_op_argument_errors():
     assert lib.tsa_gdn_gated_rmsnorm(DUMMY, DUMMY, DUMMY, DUMMY, 1, 2, 3, 64, 1e-6, NULL) == tsa.TSA_ERR_UNSUPPORTED
     assert lib.tsa_gdn_gated_rmsnorm(DUMMY, DUMMY, DUMMY, DUMMY, 1, 0, 3, 128, 1e-6, NULL) == tsa.TSA_ERR_SHAPE
     assert lib.tsa_gdn_gated_rmsnorm(DUMMY, DUMMY, DUMMY, DUMMY, 1, 2, 3, 128, inf, NULL) == tsa.TSA_ERR_ARG
+
+
+def _tt(ne, typ=0, data=0x1000, nb=None):
+    t = tsa.TsaTensor()
+    t.data = data
+    t.type = typ
+    es = 2 if typ == 1 else 4
+    if nb is None:
+        nb = [es]
+        for i in range(3):
+            nb.append(nb[-1] * ne[i])
+    for i in range(4):
+        t.ne[i] = ne[i]
+        t.nb[i] = nb[i]
+    return t
+
+
+def test_ggml_adapter_argument_errors():
+    lib = tsa.load()
+    B, T, Hk, Hv, S = 1, 8, 2, 4, 128
+
+    def call(**over):
+        d = dict(q=_tt([S, Hk, T, B]), k=_tt([S, Hk, T, B]), v=_tt([S, Hv, T, B]),
+                 g=_tt([Hv, T, B, 1]), beta=_tt([Hv, T, B, 1]), state=_tt([S, S, Hv, B]),
+                 out=_tt([S, Hv, T, B]), state_out=_tt([S, S, Hv, B], data=0x2000))
+        scale = over.pop("scale", 0.1)
+        ws = over.pop("ws", DUMMY)
+        d.update(over)
+        args = [ctypes.byref(d[n]) if d[n] is not None else None
+                for n in ("q", "k", "v", "g", "beta", "state", "out", "state_out")]
+        return lib.tsa_ggml_gated_delta_net(*args, scale, ws, 1 << 40, NULL)
+
+    assert call(k=None) == tsa.TSA_ERR_NULL
+    assert call(v=_tt([S, Hv, T, B], data=0)) == tsa.TSA_ERR_NULL
+    assert call(q=_tt([S, Hk, T, B], typ=7)) == tsa.TSA_ERR_ARG
+    assert call(g=_tt([Hv, T, B, 1], typ=1)) == tsa.TSA_ERR_UNSUPPORTED   # gates are fp32
+    assert call(state=_tt([S, S, Hv, B], typ=1)) == tsa.TSA_ERR_UNSUPPORTED
+    assert call(k=_tt([S, Hk + 1, T, B])) == tsa.TSA_ERR_SHAPE
+    assert call(out=_tt([S, Hv, T + 1, B])) == tsa.TSA_ERR_SHAPE
+    assert call(beta=_tt([Hv, T, B, 2])) == tsa.TSA_ERR_SHAPE
+    assert call(q=_tt([S, Hk, 0, B]), k=_tt([S, Hk, 0, B])) == tsa.TSA_ERR_SHAPE
+    q64 = _tt([64, Hk, T, B])
+    assert call(q=q64, k=_tt([64, Hk, T, B]), state=_tt([64, S, Hv, B]),
+                state_out=_tt([64, S, Hv, B], data=0x2000)) == tsa.TSA_ERR_UNSUPPORTED
+    assert call(scale=float("nan")) == tsa.TSA_ERR_ARG
+    # in place must be the same view
+    assert call(state_out=_tt([S, S, Hv, B], nb=[4, 1024, 65536, 4 * 65536])) == tsa.TSA_ERR_ARG
+    assert call(ws=NULL) == tsa.TSA_ERR_WORKSPACE
+
+
+def test_ggml_workspace_bytes():
+    lib = tsa.load()
+    ws = lambda T, Hk=2, Hv=4, S=128: lib.tsa_ggml_gdn_workspace_bytes(
+        ctypes.byref(_tt([S, Hk, T, 1])), ctypes.byref(_tt([S, Hv, T, 1])))
+    assert ws(8, S=64) == 0 and ws(0) == 0
+    small, big = ws(31), ws(32)
+    # from 32 tokens on (the chunked prefill's dispatch), its workspace is included
+    assert big - small >= tsa.gdn_chunked_workspace_bytes(1, 32, 2, 4)
+    assert ws(128) > ws(64) > 0

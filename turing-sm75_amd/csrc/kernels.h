@@ -43,6 +43,15 @@ hipError_t gdn_preprocess(const void* q, const void* k, const float* a, const fl
                           hipStream_t stream);
 hipError_t gdn_gated_rmsnorm(const void* x, const void* z, const float* w, void* y, int B, int T,
                              int Hv, float eps, hipStream_t stream);
+// A strided 4-D view: ne[0] innermost, nb[i] byte strides (ggml's convention).
+struct View4 {
+    long long ne[4];
+    long long nb[4];
+};
+// dst(view d, type dst_f16 ? fp16 : fp32) <- src(view s, likewise); d.ne must equal s.ne.
+hipError_t copy4d(const void* src, int src_f16, const View4& s, void* dst, int dst_f16,
+                  const View4& d, hipStream_t stream);
+
 hipError_t gdn_naive(const void* q, const void* k, const void* v, const float* g_log,
                      const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
                      int dk, int dv, float scale, hipStream_t stream);

@@ -32,6 +32,18 @@ TSA_ERR_WORKSPACE = 4
 TSA_ERR_LAUNCH = 5
 TSA_ERR_ARG = 6
 
+TSA_TYPE_F32, TSA_TYPE_F16 = 0, 1
+
+
+class TsaTensor(ctypes.Structure):
+    """The tsa_tensor view of include/tsa.h (the fields of a ggml_tensor view)."""
+    _fields_ = [("data", ctypes.c_void_p), ("type", ctypes.c_int),
+                ("ne", ctypes.c_int64 * 4), ("nb", ctypes.c_size_t * 4)]
+
+
+_tp = ctypes.POINTER(TsaTensor)
+
+
 _vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 _SIGNATURES = {
     "tsa_strerror": (ctypes.c_char_p, [_i]),
@@ -49,6 +61,8 @@ _SIGNATURES = {
     "tsa_gdn_decode_fused_step": (_i, [_vp] * 9 + [_i] * 5 + [_f, _f, _vp]),
     "tsa_gdn_preprocess": (_i, [_vp] * 10 + [_i] * 5 + [_f, _vp]),
     "tsa_gdn_gated_rmsnorm": (_i, [_vp] * 4 + [_i] * 4 + [_f, _vp]),
+    "tsa_ggml_gdn_workspace_bytes": (_sz, [_tp, _tp]),
+    "tsa_ggml_gated_delta_net": (_i, [_tp] * 8 + [_f, _vp, _sz, _vp]),
 }
 
 
@@ -341,4 +355,50 @@ def gdn_gated_rmsnorm(x, z, w, out=None, eps=1e-6, stream=None):
     B, T, Hv, dv = x.shape
     _check(load().tsa_gdn_gated_rmsnorm(_ptr(x), _ptr(z), _ptr(w), _ptr(out), B, T, Hv, dv,
                                         float(eps), _stream(stream)))
+    return out
+
+
+# ---- ggml-layout adapter ----
+def ggml_view(t) -> TsaTensor:
+    """The ggml view of a torch tensor of up to 4 dims: ne / nb are its shape / strides in
+    reverse order (ne[0] = the innermost dimension), padded with 1s."""
+    import torch
+    if t.dtype not in (torch.float32, torch.float16):
+        raise ValueError(f"ggml views are fp32 or fp16, got {t.dtype}")
+    if t.dim() > 4 or not t.is_cuda:
+        raise ValueError("a ggml view is a CUDA tensor of at most 4 dims")
+    ne = list(reversed(t.shape)) + [1] * (4 - t.dim())
+    es = t.element_size()
+    nb = [st * es for st in reversed(t.stride())]
+    while len(nb) < 4:
+        nb.append(nb[-1] * ne[len(nb) - 1] if nb else es)
+    v = TsaTensor()
+    v.data = t.data_ptr()
+    v.type = TSA_TYPE_F16 if t.dtype == torch.float16 else TSA_TYPE_F32
+    for i in range(4):
+        v.ne[i] = int(ne[i])
+        v.nb[i] = int(nb[i])
+    return v
+
+
+def ggml_gdn_workspace_bytes(q, v) -> int:
+    return int(load().tsa_ggml_gdn_workspace_bytes(ctypes.byref(ggml_view(q)), ctypes.byref(ggml_view(v))))
+
+
+def ggml_gated_delta_net(q, k, v, g_log, beta, state, out, state_out=None, scale=None, ws=None,
+                         stream=None):
+    """Torch tensors in the kernels' index order ([B, T, H, S] for q / k / v / out,
+    [B, T, Hv] for g_log / beta, [B, Hv, S, S] for the states), any strides / fp32 or fp16:
+    passed as ggml views.  state_out defaults to state (in place)."""
+    import torch
+    if state_out is None:
+        state_out = state
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    views = [ggml_view(x) for x in (q, k, v, g_log, beta, state, out, state_out)]
+    need = int(load().tsa_ggml_gdn_workspace_bytes(ctypes.byref(views[0]), ctypes.byref(views[2])))
+    if ws is None:
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    _check(load().tsa_ggml_gated_delta_net(*[ctypes.byref(x) for x in views], float(scale),
+                                           _ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))
     return out
