@@ -231,6 +231,23 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                 if (kk == C::kKSteps / 2 - 1 && more)
                     copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
             }
+            // V^T operands of the first key step, read now so that their LDS time runs under
+            // the softmax (V does not depend on P); a wave reads transposed V at only ~18 B/clk.
+            // At D = 256 the registers are not there (one wave per SIMD already).
+            constexpr bool kPreV = D <= 128;
+            auto read_v = [&](int ks, int db) {
+                const int r0 = 16 * ks + 4 * hi + vj;      // e = 0 row
+                const int r1 = r0 + 8;                       // e = 1 row
+                const int ch = 4 * db + vchunk;
+                const half4_t lo = lds_read_tr16(Vt + r0 * D + chunk_pos<D>(r0, ch) * 8 + vsub);
+                const half4_t up = lds_read_tr16(Vt + r1 * D + chunk_pos<D>(r1, ch) * 8 + vsub);
+                return half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+            };
+            half8_t v0[kPreV ? C::kDBlocks : 1];
+            if (kPreV) {
+#pragma unroll
+                for (int db = 0; db < C::kDBlocks; ++db) v0[db] = read_v(0, db);
+            }
             // ---- masks: causal diagonal and keys past S ----
             if ((kCausal && k0 + kKRows - 1 > qw0) || k0 + kKRows > S) {
 #pragma unroll
@@ -282,15 +299,8 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                 if (ks == 1 && more)
                     copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
 #pragma unroll
-                for (int db = 0; db < C::kDBlocks; ++db) {
-                    const int r0 = 16 * ks + 4 * hi + vj;      // e = 0 row
-                    const int r1 = r0 + 8;                       // e = 1 row
-                    const int ch = 4 * db + vchunk;
-                    const half4_t lo = lds_read_tr16(Vt + r0 * D + chunk_pos<D>(r0, ch) * 8 + vsub);
-                    const half4_t up = lds_read_tr16(Vt + r1 * D + chunk_pos<D>(r1, ch) * 8 + vsub);
-                    const half8_t a = {lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-                    o[db] = mfma32(a, p[ks], o[db]);
-                }
+                for (int db = 0; db < C::kDBlocks; ++db)
+                    o[db] = mfma32(kPreV && ks == 0 ? v0[kPreV ? db : 0] : read_v(ks, db), p[ks], o[db]);
             }
             __builtin_amdgcn_s_setprio(0);
         }
