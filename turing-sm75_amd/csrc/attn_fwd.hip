@@ -132,7 +132,9 @@ __device__ __forceinline__ void copy_tile(const unsigned (&off)[Dma<D>::kPerWave
                       lds_buf + (unsigned)(isv ? kKRows * D * 2 : 0) + 1024u * blk);
         }
     };
-    if (lastrow >= kKRows - 1)
+    // At D = 256 every register counts (one wave per SIMD, the PV loop waits on each V read
+    // when none is free to read ahead): there the offsets are recomputed per copy.
+    if (lastrow >= kKRows - 1 && D <= 128)
         issue_all(std::false_type{});
     else
         issue_all(std::true_type{});
@@ -196,7 +198,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
 #pragma unroll
     for (int j = 0; j < Dma<D>::kPerWave; ++j) {
         const int n = wave + 4 * j;
-        off[j] = dma_off<D>(n >= Dma<D>::kTile ? n - Dma<D>::kTile : n, lane, kKRows - 1);
+        off[j] = D <= 128 ? dma_off<D>(n >= Dma<D>::kTile ? n - Dma<D>::kTile : n, lane, kKRows - 1) : 0u;
     }
     const unsigned lds0 = (unsigned)(uintptr_t)(lds_void_t)(void*)lds;
     const unsigned buf_bytes = 2 * C::kTile * 2;
@@ -204,7 +206,18 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, 0, S, lds0);
     dma_wait_barrier();
 
+    // At D = 256 (one wave per SIMD, registers full) the allocator otherwise parks O in VGPRs
+    // during the QK^T part and copies all 128 accumulators between VGPRs and AGPRs twice per
+    // tile; an empty asm with an AGPR constraint at both ends of the PV block keeps O in
+    // AGPRs, where the MFMAs accumulate directly.
+    auto pin_o = [&]() {
+        if (D == 256) {
+#pragma unroll
+            for (int i = 0; i < C::kDBlocks; ++i) asm volatile("" : "+a"(o[i]));
+        }
+    };
     for (int t = 0; t < n_tiles; ++t) {
+        pin_o();
         const int k0 = t * kKRows;
         const bool more = t + 1 < n_tiles;
         const unsigned nbuf = lds0 + ((t + 1) & 1) * buf_bytes;
@@ -303,6 +316,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                     o[db] = mfma32(kPreV && ks == 0 ? v0[kPreV ? db : 0] : read_v(ks, db), p[ks], o[db]);
             }
             __builtin_amdgcn_s_setprio(0);
+            pin_o();
         }
         dma_wait_barrier();
     }
