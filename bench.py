@@ -249,8 +249,8 @@ def main():
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the hot path's sharding (heads / sequences) is "
-              "described in DESIGN.md and no multi-GPU figure is produced", file=sys.stderr)
+        print("bench.py measures one GPU: sharding this path over GPUs (heads or sequences, "
+              "no exchange) is design-only and no multi-GPU figure is produced", file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)

@@ -2,8 +2,9 @@
 
 Gate: max-abs error < 0.02 on fp16 outputs (the reference's gate, src/attn_sm75.cu:501-502);
 a tighter 5e-3 bound guards against regressions that the gate would still let through.
-Cases: the float64 fixtures, BASELINE configs 1-3 (config 3 against a seeded sample of
-oracle rows plus the full on-device naive kernel), the reference's own inputs
+Cases: the float64 fixtures, B=1 H=4 S=256 D=128 non-causal, B=2 H=8 S=512 causal at D=64 and
+128, B=1 H=32 S=8192 D=128 causal with outliers (against a seeded sample of oracle rows plus
+the full on-device naive kernel), the reference's own inputs
 (mt19937(42), N(0, 0.5), src/attn_sm75.cu:398,473-476), ragged S, and size-independent
 properties at full size (row 0 of a causal head is V[0] exactly).
 """
@@ -46,20 +47,20 @@ def test_golden_fixtures(dev, golden, i):
     assert _err(o, g[f"c{i}_o"]) < TIGHT
 
 
-def test_config1_noncausal(dev, orc):
+def test_b1_h4_s256_d128_noncausal(dev, orc):
     rng = np.random.default_rng(101)
     q, k, v = (_normal(rng, (1, 4, 256, 128)) for _ in range(3))
     e = _err(_run(dev, q, k, v, False), orc.attn_naive(q, k, v, False))
-    print(f"config1 max-abs {e:.5f}")
+    print(f"B=1 H=4 S=256 D=128 non-causal max-abs {e:.5f}")
     assert e < TIGHT
 
 
 @pytest.mark.parametrize("D", [64, 128])
-def test_config2_causal(dev, orc, D):
+def test_b2_h8_s512_causal(dev, orc, D):
     rng = np.random.default_rng(102 + D)
     q, k, v = (_normal(rng, (2, 8, 512, D)) for _ in range(3))
     e = _err(_run(dev, q, k, v, True), orc.attn_naive(q, k, v, True))
-    print(f"config2 D={D} max-abs {e:.5f}")
+    print(f"B=2 H=8 S=512 D={D} causal max-abs {e:.5f}")
     assert e < TIGHT
 
 
@@ -85,7 +86,7 @@ def test_ragged_lengths(dev, orc, S, D, causal):
     assert _err(_run(dev, q, k, v, causal), orc.attn_naive(q, k, v, causal)) < TIGHT
 
 
-def test_config3_long_context_outliers(dev, orc):
+def test_b1_h32_s8192_d128_causal_outliers(dev, orc):
     """B=1 H=32 S=8192 D=128 causal, N(0, 0.5) with 1% of entries x8."""
     import torch
     rng = np.random.default_rng(103)
@@ -109,7 +110,7 @@ def test_config3_long_context_outliers(dev, orc):
     rows = np.concatenate([rng.integers(0, 32 * S, 320), [0, S - 1, 5 * S, 31 * S + S - 1, 17 * S + 4095]])
     rows, _, o16 = orc.attn_rows(q, k, v, np.unique(rows), True)
     e_orc = _err(o_np.reshape(-1, 128)[rows], o16)
-    print(f"config3 max-abs vs naive kernel {e_naive:.5f}, vs oracle rows {e_orc:.5f}")
+    print(f"B=1 H=32 S=8192 D=128 causal max-abs vs naive kernel {e_naive:.5f}, vs oracle rows {e_orc:.5f}")
     assert e_orc < GATE and e_naive < GATE
     assert e_orc < TIGHT
     # size-independent property: a causal row 0 attends only to key 0, so O[0] = V[0]

@@ -3,11 +3,11 @@
 
 Gates: outputs max-abs < 0.02 (fp16 I/O, src/gdn_sm75.cu:1313) and the fp32 state within
 1e-3 relative (max |dS| / max |S|).  Tighter bounds guard each kernel's expected accuracy.
-Cases: float64 fixtures; BASELINE config 4 (T=4096, Hq=16, Hv=32, C=64) in full; the
+Cases: float64 fixtures; the T=4096, Hq=16, Hv=32, C=64 prefill in full; the
 reference driver's LCG inputs and shape (Hv=48, T=512); ragged T and head maps with
-Hv % Hq != 0; batches; state continuity across calls (prefill -> prefill -> decode); BASELINE
-config 5 (16 sequences x 32 heads, N(0, 0.02) state) over 64 steps in full and 512 steps on a
-subset of sequences.
+Hv % Hq != 0; batches; state continuity across calls (prefill -> prefill -> decode); the
+decode step of 16 sequences x 32 heads (N(0, 0.02) state) over 64 steps in full and 512 steps
+on a subset of sequences.
 """
 import numpy as np
 import pytest
@@ -72,12 +72,12 @@ def test_golden_fixtures(dev, golden, kind, i):
 
 
 @pytest.mark.parametrize("kind", ["chunked", "recurrent"])
-def test_config4_full(dev, orc, kind):
+def test_t4096_hq16_hv32_full(dev, orc, kind):
     rng = np.random.default_rng(401)
     q, k, v, g, beta, st = _inputs(rng, 1, 4096, 16, 32)
     o, s = _gpu(dev, kind, q, k, v, g, beta, st)
     o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
-    _check(o, s, o_ref, s_ref, *TOL[kind], label=f"{kind} config4")
+    _check(o, s, o_ref, s_ref, *TOL[kind], label=f"{kind} T=4096 Hq=16 Hv=32")
 
 
 @pytest.mark.parametrize("kind", ["chunked", "recurrent"])
@@ -134,7 +134,7 @@ def _decode_run(dev, q, k, v, g, beta, st):
     return o, ts.cpu().numpy()
 
 
-def test_config5_decode_64_steps_full(dev, orc):
+def test_decode_b16_hv32_64_steps_full(dev, orc):
     rng = np.random.default_rng(501)
     q, k, v, g, beta, st = _inputs(rng, 16, 64, 16, 32, sstd=0.02)
     o, s = _decode_run(dev, q, k, v, g, beta, st)
@@ -142,7 +142,7 @@ def test_config5_decode_64_steps_full(dev, orc):
     _check(o, s, o_ref, s_ref, 2e-3, 1e-5, label="decode 16x32 heads, 64 steps")
 
 
-def test_config5_decode_512_steps_subset(dev, orc):
+def test_decode_b16_hv32_512_steps_subset(dev, orc):
     rng = np.random.default_rng(502)
     q, k, v, g, beta, st = _inputs(rng, 16, 512, 16, 32, sstd=0.02)
     o, s = _decode_run(dev, q, k, v, g, beta, st)

@@ -7,8 +7,8 @@ Inputs are the raw quantities of the layer: q, k ~ N(0,1) rows (not normalised),
 projections a, b ~ N(0,1), dt_bias ~ N(0, 0.5), A = -exp(N(0, 0.5)).  Gates: the recurrence
 gates (outputs max-abs < 0.02, state within 1e-3 relative); the pre-op outputs are fp16
 rows of unit norm (abs 2e-3) and fp32 gates (rel 1e-5); the post-op output abs 2e-2 /
-rel 1e-2 of an fp16 value.  Cases: shapes of the target model's layer and BASELINE config 4
-(T=4096, Hq=16, Hv=32), ragged T, Hv % Hq != 0, batches, in-place forms, decode continuity.
+rel 1e-2 of an fp16 value.  Cases: shapes of the target model's layer and the T=4096, Hq=16, Hv=32
+prefill, ragged T, Hv % Hq != 0, batches, in-place forms, decode continuity.
 """
 import numpy as np
 import pytest
@@ -105,7 +105,7 @@ CASES = [  # B, T, Hq, Hv
     (1, 100, 3, 5),      # ragged T, Hv % Hq != 0
     (2, 130, 2, 6),      # batch, ragged
     (1, 1, 1, 1),
-    (1, 4096, 16, 32),   # BASELINE config 4 from raw inputs
+    (1, 4096, 16, 32),   # the T=4096, Hq=16, Hv=32 prefill from raw inputs
 ]
 
 

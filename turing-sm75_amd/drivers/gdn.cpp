@@ -1,6 +1,6 @@
 // gdn -- the Gated DeltaNet lab driver, rebuilt over the tsa C-ABI.
 //
-//   gdn [T] [--hv 48] [--hq 16] [--batch B] [--dist lcg|baseline] [--mode prefill|decode]
+//   gdn [T] [--hv 48] [--hq 16] [--batch B] [--dist lcg|normal] [--mode prefill|decode]
 //       [--steps N] [--seed N] [--iters N]
 //
 // Mirrors main() of src/gdn_sm75.cu:1246-1412: T (default 64), shape d = 128, Hq = 16,
@@ -8,7 +8,7 @@
 // values are rounded to fp16 for q/k/v, the library's I/O type), state zero, every kernel
 // checked against the naive kernel (max |out - naive| < 0.02, plus the fp32 state within
 // 1e-3 relative), state reset before each checked launch (:1316), 20 timed launches,
-// "ms x48 layers" (:1331).  --dist baseline draws q, k ~ N(0,1) with L2-normalised rows,
+// "ms x48 layers" (:1331).  --dist normal draws q, k ~ N(0,1) with L2-normalised rows,
 // v ~ N(0,1), beta = sigmoid(N(0,1)), g_log = -softplus(N(0,1)).  --mode decode runs
 // --steps single-token steps for --batch sequences from a N(0, 0.02) state.
 #include <algorithm>
@@ -96,11 +96,11 @@ int main(int argc, char** argv) {
     Opts opt(argc, argv);
     if (opt.bad || opt.pos.size() > 1 ||
         !opt.known({"hv", "hq", "batch", "dist", "mode", "steps", "seed", "iters"})) {
-        std::fprintf(stderr, "usage: %s [T] [--hv N] [--hq N] [--batch B] [--dist lcg|baseline] [--mode prefill|decode] [--steps N] [--seed N] [--iters N]\n", argv[0]);
+        std::fprintf(stderr, "usage: %s [T] [--hv N] [--hq N] [--batch B] [--dist lcg|normal] [--mode prefill|decode] [--steps N] [--seed N] [--iters N]\n", argv[0]);
         return 2;
     }
     const std::string mode = opt.get("mode", "prefill");
-    const std::string dist = opt.get("dist", mode == "decode" ? "baseline" : "lcg");
+    const std::string dist = opt.get("dist", mode == "decode" ? "normal" : "lcg");
     int T = opt.pos.empty() ? 64 : std::atoi(opt.pos[0].c_str());
     const int Hv = std::atoi(opt.get("hv", "48").c_str());
     const int Hq = std::atoi(opt.get("hq", "16").c_str());
@@ -110,7 +110,7 @@ int main(int argc, char** argv) {
     const int iters = std::atoi(opt.get("iters", "20").c_str());
     const int d = 128;
     if (T < 1 || Hv < 1 || Hq < 1 || B < 1 || steps < 1 || iters < 1 ||
-        (mode != "prefill" && mode != "decode") || (dist != "lcg" && dist != "baseline")) {
+        (mode != "prefill" && mode != "decode") || (dist != "lcg" && dist != "normal")) {
         std::fprintf(stderr, "usage: %s [T] ... (T, heads, batch, steps >= 1)\n", argv[0]);
         return 2;
     }
