@@ -27,6 +27,9 @@
 //   ahead with gfx950 LDS-DMA (global_load_lds_dwordx4) into double-buffered slots, so no
 //   register holds prefetched data and each wave reads its MFMA operands from LDS in
 //   batches ahead of the MFMAs.
+#include <atomic>
+#include <mutex>
+#include <random>
 #include <type_traits>
 
 #include "common.h"
@@ -50,6 +53,14 @@ constexpr int kWsAqk = kWsU + kC * kD * 2;  // fp16 [64 t][64]: column s stored 
 // qn_t, kn_t are the l2-norm factors of the fused entry point's raw q / k rows (1 otherwise)
 constexpr int kWsG = kWsAqk + kC * kC * 2;
 constexpr int kWsChunk = kWsG + kC * 16;    // 41984 B, multiple of 256
+
+// Ready flags, after all chunk workspaces: one word per (b, h, chunk).  The prep writes the
+// call's epoch there once the chunk's workspace is in memory; the carry's DMA waves wait
+// for it before copying the chunk.  Epochs differ from call to call, so flags left by an
+// earlier call never read as ready and nothing has to clear them.
+// A wait gives up after kSpinMax polls (a few tenths of a second) and the carry then
+// writes NaN state instead of hanging.
+constexpr int kSpinMax = 1 << 18;
 
 // Within each aligned 32-block, index 16a + 4g + b is stored at 8g + 4a + b.  A 16x16x32
 // MFMA lane of group g then finds its 8 k-values {16a + 4g + b} in one 16-byte run; that
@@ -86,6 +97,21 @@ __device__ __forceinline__ half8_t cat8(const half4_t& a, const half4_t& b) {
     return half8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// Device-scope stores of the workspace (sc1): written through to the device's coherence
+// point, so the carry, whose copies of them are device-scope loads too, sees them from any
+// XCD as soon as this wave's vmcnt has drained -- no L2 write-back or invalidate needed
+// (both measured far too slow to issue once per workgroup or chunk).
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_dev(unsigned char* p, const uint4& v) {
+    const u32x4_t x = {v.x, v.y, v.z, v.w};
+    // s_nop 1: a store of more than 8 bytes may still read its data registers in the next
+    // cycle, and the compiler does not see into this asm to keep them unchanged that long
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p), "v"(x) : "memory");
+}
+__device__ __forceinline__ void store_dev(float* p, float v) {
+    asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+
 // ----------------------------------------------------------------------------------
 // Prep
 // ----------------------------------------------------------------------------------
@@ -116,11 +142,13 @@ __global__ void __launch_bounds__(kThreads, 3)
 gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
                const half_t* __restrict__ v, const float* __restrict__ g_log,
                const float* __restrict__ beta, GdnRawGates gates, unsigned char* __restrict__ ws,
-               int T, int Hq, int Hv, int nch) {
+               unsigned* __restrict__ flags, unsigned epoch, int T, int Hq, int Hv, int nch, int BHv) {
     __shared__ PrepLds sm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hi = lane >> 5;
-    const int ch = blockIdx.x % nch;
-    const int bh = blockIdx.x / nch;
+    // chunk-major: workgroups are dispatched in the order the carry consumes chunks, and
+    // (b, h, chunk) lands on the XCD of the head's carry workgroups when BHv % 8 == 0
+    const int ch = blockIdx.x / BHv;
+    const int bh = blockIdx.x % BHv;
     const int b = bh / Hv, h = bh % Hv, hq = h % Hq;
     const int t0 = ch * kC;
     unsigned char* wsc = ws + ((size_t)bh * nch + ch) * kWsChunk;
@@ -235,8 +263,7 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int id = it * kThreads + tid;
-        *reinterpret_cast<uint4*>(wsc + kWsAqk + (size_t)id * 16) =
-            *reinterpret_cast<const uint4*>(sm.Aqk + id * 8);
+        store_dev(wsc + kWsAqk + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.Aqk + id * 8));
     }
     if (wave == 1) {
         const float x = sm.G[lane], xc = sm.G[kC - 1];
@@ -244,10 +271,10 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
         const float kn = kFused ? sm.kn[lane] : 1.f, qn = kFused ? sm.qn[lane] : 1.f;
         sm.bg[lane] = sm.bt[lane] * ex * kn;
         float* wg = reinterpret_cast<float*>(wsc + kWsG);
-        wg[lane] = ex * qn;
-        wg[kC + lane] = __expf(xc - x) * kn;
-        wg[2 * kC + lane] = lane == 0 ? __expf(xc) : 0.f;
-        wg[3 * kC + lane] = 0.f;
+        store_dev(wg + lane, ex * qn);
+        store_dev(wg + kC + lane, __expf(xc - x) * kn);
+        store_dev(wg + 2 * kC + lane, lane == 0 ? __expf(xc) : 0.f);
+        store_dev(wg + 3 * kC + lane, 0.f);
     }
     lds_barrier();
     if (wave == 0) {  // the four 16x16 diagonal blocks, one column per lane
@@ -359,9 +386,15 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int id = it * kThreads + tid;
-        *reinterpret_cast<uint4*>(wsc + kWsW + (size_t)id * 16) = *reinterpret_cast<const uint4*>(sm.Wst + id * 8);
-        *reinterpret_cast<uint4*>(wsc + kWsU + (size_t)id * 16) = *reinterpret_cast<const uint4*>(sm.Ust + id * 8);
+        store_dev(wsc + kWsW + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.Wst + id * 8));
+        store_dev(wsc + kWsU + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.Ust + id * 8));
     }
+
+    // ---- 6. publish: every wave's device-scope stores complete, then the chunk's flag ----
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    if (tid == 0)
+        __hip_atomic_store(flags + (size_t)bh * nch + ch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------------------------------------
@@ -386,6 +419,7 @@ struct CarryLds {
     OutSlot os[2];
     uint4 XS[2][kStrips][6][64];     // chain -> output: S operands (4) and Vnew operands (2)
     half_t OS[2][32 * 32];           // per output wave: its 32 tokens x 32 columns of O
+    int err[4];                      // per DMA wave: a ready wait timed out
 };
 
 // 16-B chunk swizzle of the [64][64] Aqk tile: 16 consecutive rows at one chunk are
@@ -435,10 +469,17 @@ __device__ __forceinline__ unsigned dma_src_off(int n, int lane, unsigned rowbyt
 // offset).  Written as inline asm on purpose: the compiler does not track LDS written by
 // DMA slot by slot and would wait for every DMA in flight before the first LDS read of the
 // other slot; the kernel orders the copies and the reads itself (dma_wait_barrier).
-__device__ __forceinline__ void dma_issue(const void* base, unsigned off, unsigned lds_addr, bool half) {
-    if (!half || (threadIdx.x & 63) < 32)
-        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(off), "s"(base), "{m0}"(lds_addr)
-                     : "memory");
+// Workspace tiles (dev) are device-scope loads (sc1), the counterpart of the prep's stores.
+__device__ __forceinline__ void dma_issue(const void* base, unsigned off, unsigned lds_addr, bool half,
+                                          bool dev) {
+    if (!half || (threadIdx.x & 63) < 32) {
+        if (dev)
+            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 sc1" :: "v"(off), "s"(base),
+                         "{m0}"(lds_addr) : "memory");
+        else
+            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(off), "s"(base),
+                         "{m0}"(lds_addr) : "memory");
+    }
 }
 
 // Wait for this wave's copies (vmcnt counts them), then a barrier over LDS: after it every
@@ -456,6 +497,7 @@ __device__ __forceinline__ void dma_wait_barrier() {
 template <int W>
 __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const unsigned char* kh,
                                          const unsigned char* qh, const unsigned char* wsh,
+                                         const unsigned* fl, unsigned epoch, int* err,
                                          unsigned rowbytes, int pair, int T, int nch) {
     constexpr int kJ = (kDmaN - W + 3) / 4;
     const int lane = threadIdx.x & 63;
@@ -483,7 +525,7 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
                     o = dma_src_off(n, lane, rowbytes, pair, chainslot ? last_c : last_o);
                 const unsigned char* base = chainslot ? (rows ? kb : wc) : (rows ? qb : wo);
                 const unsigned lds = (chainslot ? slot_lds[pc] : slot_lds[2 + po]) + 1024u * i;
-                dma_issue(base, o, lds, n == kDmaEOut);
+                dma_issue(base, o, lds, n == kDmaEOut, !rows);
             }
         };
         if ((do_c && last_c < kC - 1) || (do_o && last_o < kC - 1))
@@ -491,13 +533,39 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
         else
             issue_all(std::false_type{});
     };
+    // fl[n] is chunk n's flag (device-scope loads, like the workspace copies that follow
+    // it).  The flag of the next chunk is loaded right after a chunk's copies are issued, so
+    // its round trip overlaps them and a chunk that is ready costs no wait.  After one
+    // timed-out wait, no more waits.
+    auto peek = [&](int n) -> unsigned {
+        return n < nch ? __hip_atomic_load(fl + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+    };
+    auto ready = [&](int n, unsigned v) {
+        v = __builtin_amdgcn_readfirstlane(v);
+        for (int s = 0; v != epoch && !*err; ++s) {
+            if (s == kSpinMax) {
+                *err = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(8);
+            v = __builtin_amdgcn_readfirstlane(
+                __hip_atomic_load(fl + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        }
+    };
+    *err = 0;
+    ready(0, peek(0));
     copies(0, 0, 0, -1);
+    unsigned nxt = peek(1);
     dma_wait_barrier();
     for (int it = 0; it <= nch; it += 2) {
+        if (it + 1 < nch) ready(it + 1, nxt);
         copies(1, 0, it + 1, it);
+        nxt = peek(it + 2);
         dma_wait_barrier();
         if (it + 1 > nch) break;
+        if (it + 2 < nch) ready(it + 2, nxt);
         copies(0, 1, it + 2, it + 1);
+        nxt = peek(it + 3);
         dma_wait_barrier();
     }
 }
@@ -668,8 +736,9 @@ __device__ __forceinline__ void out_flush(const half_t* ostage, half_t* out, int
 
 __global__ void __launch_bounds__(kCarryThreads, 1)
 gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
-                const unsigned char* __restrict__ ws, float* __restrict__ state,
-                half_t* __restrict__ out, int T, int Hq, int Hv, int nch, int BHv, float scale) {
+                const unsigned char* __restrict__ ws, const unsigned* __restrict__ flags,
+                unsigned epoch, float* __restrict__ state, half_t* __restrict__ out, int T, int Hq, int Hv,
+                int nch, int BHv, float scale) {
     __shared__ CarryLds sm;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: role branches are scalar
@@ -728,17 +797,23 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.cs[1],
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.os[0],
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.os[1]};
+        const unsigned* fl = flags + (size_t)bh * nch;
+        int* err = &sm.err[wave - 4];
         switch (wave) {
-            case 4: dma_role<0>(slot_lds, kh, qh, wsh, rowbytes, pair, T, nch); break;
-            case 5: dma_role<1>(slot_lds, kh, qh, wsh, rowbytes, pair, T, nch); break;
-            case 6: dma_role<2>(slot_lds, kh, qh, wsh, rowbytes, pair, T, nch); break;
-            default: dma_role<3>(slot_lds, kh, qh, wsh, rowbytes, pair, T, nch); break;
+            case 4: dma_role<0>(slot_lds, kh, qh, wsh, fl, epoch, err, rowbytes, pair, T, nch); break;
+            case 5: dma_role<1>(slot_lds, kh, qh, wsh, fl, epoch, err, rowbytes, pair, T, nch); break;
+            case 6: dma_role<2>(slot_lds, kh, qh, wsh, fl, epoch, err, rowbytes, pair, T, nch); break;
+            default: dma_role<3>(slot_lds, kh, qh, wsh, fl, epoch, err, rowbytes, pair, T, nch); break;
         }
     }
     if (chain) {
+        // a timed-out wait means the chunk operands were never published: poison the state
+        const bool lost = (sm.err[0] | sm.err[1] | sm.err[2] | sm.err[3]) != 0;
+        const float nan = __builtin_nanf("");
 #pragma unroll
         for (int m = 0; m < 8; ++m)
-            *reinterpret_cast<float4*>(Sg + 16 * m + 4 * g) = make_float4(S[m][0], S[m][1], S[m][2], S[m][3]);
+            *reinterpret_cast<float4*>(Sg + 16 * m + 4 * g) =
+                lost ? make_float4(nan, nan, nan, nan) : make_float4(S[m][0], S[m][1], S[m][2], S[m][3]);
     } else if (outw) {
         out_flush(sm.OS[wave - 2], out, b, T, Hv, h, (nch - 1) * kC, pair, wave - 2);
     }
@@ -748,27 +823,93 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
 
 size_t gdn_chunked_ws_bytes(int B, int T, int Hv) {
     const size_t nch = (size_t)(T + kC - 1) / kC;
-    return (size_t)B * Hv * nch * kWsChunk;
+    return (size_t)B * Hv * nch * (kWsChunk + sizeof(unsigned));
 }
 
 namespace {
+
+// The prep runs on a second stream of the device so that it overlaps the carry: the carry
+// copies a chunk's operands as soon as the prep has published them (ready flags), and the
+// chunk-major prep order produces them in the order the carry consumes them.  One side
+// stream and its fork / join events per device, created on first use.
+struct SideStream {
+    bool tried = false, ok = false;
+    int cus = 0;
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kMaxDevices = 64;
+std::mutex g_side_mu;
+SideStream g_side[kMaxDevices];
+
+// Per-process epochs, started from a random point so that flags left in memory by another
+// process are unlikely to read as this call's.
+unsigned next_epoch() {
+    static std::atomic<unsigned> counter{std::random_device{}()};
+    unsigned e = ++counter;
+    return e ? e : ++counter;
+}
+
 template <bool kFused>
 hipError_t launch_chunked(const void* q, const void* k, const void* v, const float* g_log,
                           const float* beta, const GdnRawGates& gates, float* state, void* out,
                           int B, int T, int Hq, int Hv, float scale, void* ws, hipStream_t stream) {
     const int nch = (T + kC - 1) / kC;
     const int BHv = B * Hv;
+    const int carry_wgs = BHv * (kD / (16 * kStrips));
     auto Q = static_cast<const half_t*>(q);
     auto K = static_cast<const half_t*>(k);
     auto W = static_cast<unsigned char*>(ws);
-    hipLaunchKernelGGL(gdn_chunk_prep<kFused>, dim3(BHv * nch), dim3(kThreads), 0, stream, Q, K,
-                       static_cast<const half_t*>(v), g_log, beta, gates, W, T, Hq, Hv, nch);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gdn_chunk_carry, dim3(BHv * (kD / (16 * kStrips))), dim3(kCarryThreads), 0,
-                       stream, Q, K, W, state, static_cast<half_t*>(out), T, Hq, Hv, nch, BHv,
-                       scale);
-    return hipGetLastError();
+    unsigned* flags = reinterpret_cast<unsigned*>(W + (size_t)BHv * nch * kWsChunk);
+    const unsigned epoch = next_epoch();
+    auto prep = [&](hipStream_t st) {
+        hipLaunchKernelGGL(gdn_chunk_prep<kFused>, dim3(BHv * nch), dim3(kThreads), 0, st, Q, K,
+                           static_cast<const half_t*>(v), g_log, beta, gates, W, flags, epoch, T,
+                           Hq, Hv, nch, BHv);
+        return hipGetLastError();
+    };
+    auto carry = [&]() {
+        hipLaunchKernelGGL(gdn_chunk_carry, dim3(carry_wgs), dim3(kCarryThreads), 0, stream, Q, K, W,
+                           flags, epoch, state, static_cast<half_t*>(out), T, Hq, Hv, nch, BHv,
+                           scale);
+        return hipGetLastError();
+    };
+
+    // Overlap only when it cannot stall: the carry's workgroups (one per CU) must leave at
+    // least half the CUs to the prep, and a stream being captured into a graph runs the two
+    // kernels in order (a graph does not promise to run sibling nodes concurrently).
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
+    int dev = -1;
+    SideStream* side = nullptr;
+    if (cap == hipStreamCaptureStatusNone && hipGetDevice(&dev) == hipSuccess && dev >= 0 &&
+        dev < kMaxDevices) {
+        std::lock_guard<std::mutex> lock(g_side_mu);
+        SideStream& d = g_side[dev];
+        if (!d.tried) {
+            d.tried = true;
+            d.ok = hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                   hipStreamCreateWithFlags(&d.s, hipStreamNonBlocking) == hipSuccess &&
+                   hipEventCreateWithFlags(&d.fork, hipEventDisableTiming) == hipSuccess &&
+                   hipEventCreateWithFlags(&d.join, hipEventDisableTiming) == hipSuccess;
+        }
+        if (d.ok && 2 * carry_wgs <= d.cus && nch > 1) side = &d;
+    }
+    if (!side) {
+        hipError_t e = prep(stream);
+        return e != hipSuccess ? e : carry();
+    }
+    // fork: the prep starts after the caller's earlier work; the carry is queued first so its
+    // workgroups take their CUs before the prep fills the rest; join: later work on the
+    // caller's stream (and the next call's prep) waits for this prep.
+    std::lock_guard<std::mutex> lock(g_side_mu);
+    hipError_t e = hipEventRecord(side->fork, stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side->s, side->fork, 0);
+    if (e == hipSuccess) e = carry();
+    if (e == hipSuccess) e = prep(side->s);
+    if (e == hipSuccess) e = hipEventRecord(side->join, side->s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(stream, side->join, 0);
+    return e;
 }
 }  // namespace
 
