@@ -230,18 +230,36 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
             const half_t* Kt = lds + (t & 1) * 2 * C::kTile;
             const half_t* Vt = Kt + C::kTile;
             // ---- S^T = K Q^T for two 32-key blocks, the two accumulator chains interleaved ----
+            // K operand reads: at D = 256 (one wave per SIMD, nothing else on the SIMD to run
+            // while a wave waits on LDS) they run kPreK k-steps ahead of their MFMAs, pinned
+            // there by scheduling barriers, and the first half of the next tile's copies moves
+            // to the top so that the whole QK^T block is one basic block the reads can cross.
+            // Measured on the gated GQA layer: 1.15 vs 1.23 ms causal, +8 % non-causal; at
+            // D <= 128 (two waves per SIMD) the read-ahead measured no change.
+            constexpr int kPreK = D == 256 ? 4 : 1;
+            constexpr bool kCopyTop = kPreK > 1;
+            if (kCopyTop && more)
+                copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
             float16_t s[2] = {float16_t{}, float16_t{}};
             const half_t* kr0 = Kt + krow * D;
             const half_t* kr1 = kr0 + 32 * D;
 
+            half8_t ka[C::kKSteps][2];
+            auto read_k = [&](int kk) {
+                const int cofs = ((2 * kk + hi) ^ ksw) * 8;
+                ka[kk][0] = *reinterpret_cast<const half8_t*>(kr0 + cofs);
+                ka[kk][1] = *reinterpret_cast<const half8_t*>(kr1 + cofs);
+            };
+#pragma unroll
+            for (int kk = 0; kk < kPreK; ++kk) read_k(kk);
+            if (kPreK > 1) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int kk = 0; kk < C::kKSteps; ++kk) {
-                const int cofs = ((2 * kk + hi) ^ ksw) * 8;
-                const half8_t a0 = *reinterpret_cast<const half8_t*>(kr0 + cofs);
-                const half8_t a1 = *reinterpret_cast<const half8_t*>(kr1 + cofs);
-                s[0] = mfma32(a0, qf[kk], s[0]);
-                s[1] = mfma32(a1, qf[kk], s[1]);
-                if (kk == C::kKSteps / 2 - 1 && more)
+                if (kk + kPreK < C::kKSteps) read_k(kk + kPreK);
+                s[0] = mfma32(ka[kk][0], qf[kk], s[0]);
+                s[1] = mfma32(ka[kk][1], qf[kk], s[1]);
+                if (kPreK > 1) __builtin_amdgcn_sched_barrier(0);
+                if (!kCopyTop && kk == C::kKSteps / 2 - 1 && more)
                     copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
             }
             // V^T operands of the first key step, read now so that their LDS time runs under

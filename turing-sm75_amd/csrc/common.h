@@ -49,6 +49,7 @@ __device__ __forceinline__ float dpp_mov(float x) {
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <- lane 7-i within each group of 8
+constexpr int kDppRowMirror = 0x140;  // lane i <- lane 15-i within each row of 16
 
 // Sum over each aligned group of 8 lanes; every lane of the group receives the total.
 __device__ __forceinline__ float sum8(float x) {

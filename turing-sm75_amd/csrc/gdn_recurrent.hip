@@ -14,9 +14,9 @@
 //   * the state is read and written with nontemporal loads/stores: it is touched once
 //     per launch, and keeping it out of the caches measured 4.6 -> 5.6 TB/s for the
 //     in-place read-modify-write stream of a 16 x 32 head decode step;
-//   * a 256-thread workgroup owns 32 columns of one (b, h); the 4 workgroups of a head
-//     and the B*Hv heads are independent, so a decode step of 16 x 32 heads is 2048
-//     workgroups.
+//   * T > 1: a 256-thread workgroup owns 32 columns of one (b, h) for all T tokens;
+//     decode (T = 1): a one-wave workgroup owns 8 columns, so a decode step of 16 x 32
+//     heads is 8192 independent workgroups.
 // The reference's token-serial family (serial/smem/occ/occ2/occ4/occ4p/occ8,
 // src/gdn_sm75.cu:57-188,577-893) differs only in how many columns a warp owns; here the
 // state stays fp32 (gdn_smem_kernel's fp16 state is not reproduced).
@@ -30,7 +30,8 @@ constexpr int kD = 128;          // dk = dv
 constexpr int kThreads = 256;
 constexpr int kColsPerBlock = kThreads / 8;  // 32
 constexpr int kBlocksPerHead = kD / kColsPerBlock;
-constexpr int kDecodeCols = 16;  // decode: columns per workgroup (8 threads per column)
+constexpr int kDecodeCols = 8;  // decode: columns per workgroup
+constexpr int kDecodeLpc = 8;   // decode: lanes per column
 
 __device__ __forceinline__ void load_row16(const half_t* __restrict__ p, int j, float (&x)[16]) {
     // rows 4*(it*8 + j) .. +3 for it = 0..3
@@ -101,33 +102,49 @@ gdn_recurrent_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
     for (int it = 0; it < 4; ++it) __builtin_nontemporal_store(s[it], Sc + it * 8 + j);
 }
 
-// Decode step (T = 1): one workgroup of 8 * kCols threads per kCols columns of a head, the
-// column layout of gdn_recurrent_kernel.  The q and k rows (512 bytes shared by every
-// column) come in through LDS: wave 0 loads them with one 8-byte load per lane instead of
-// every thread issuing eight.  Measured over 16 x 32 heads: 16 columns per workgroup
-// (4096 workgroups) beat 32 and 64, and walking several column blocks per workgroup with
-// the next block's state prefetched gained nothing.  kFused: q / k are raw rows, normalised
-// here (their norms come from the same 8-lane sums as the dot products), and g_log / beta
-// come from the raw projections a / b (gate arguments).
-template <int kCols, bool kFused>
-__global__ void __launch_bounds__(8 * kCols)
+// Sum over each aligned group of kLpc lanes (4, 8 or 16); every lane of the group receives it.
+template <int kLpc>
+__device__ __forceinline__ float sum_lanes(float x) {
+    x += dpp_mov<kDppXor1>(x);
+    x += dpp_mov<kDppXor2>(x);
+    if (kLpc >= 8) x += dpp_mov<kDppHalfMirror>(x);
+    if (kLpc >= 16) x += dpp_mov<kDppRowMirror>(x);
+    return x;
+}
+
+// Decode step (T = 1): one workgroup of kLpc * kCols threads per kCols columns of a head;
+// each column is owned by an aligned group of kLpc lanes, lane j holding float4 chunks
+// j, j + kLpc, ... of it.  The q and k rows (512 bytes shared by every column) come in
+// through LDS: wave 0 loads them with one 8-byte load per lane instead of every thread
+// issuing its own.  Measured over 16 x 32 heads with 16 state replicas cycled (µs per step):
+// 8 columns x 8 lanes (one wave, 8192 workgroups) 12.2, 16 x 8 12.6, 32 x 8 12.5, 8 x 16
+// 12.7, 4 x 16 12.9, 16 x 4 13.6; plain instead of nontemporal state loads / stores 15.0;
+// walking several column blocks per workgroup with the next block prefetched gained
+// nothing.  kFused: q / k are raw rows, normalised here (their norms come from the same
+// lane-group sums as the dot products), and g_log / beta come from the raw projections
+// a / b (gate arguments).
+template <int kCols, int kLpc, bool kFused>
+__global__ void __launch_bounds__(kLpc * kCols)
 gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
                   const half_t* __restrict__ v, const float* __restrict__ g_log,
                   const float* __restrict__ beta, GdnRawGates gates, float* __restrict__ state,
                   half_t* __restrict__ out, int Hq, int Hv, float scale) {
+    static_assert(kLpc * kCols >= 64, "wave 0 loads the q / k rows");
     constexpr int kWgPerHead = kD / kCols;
+    constexpr int kR = 32 / kLpc;  // float4 chunks of the column per lane
     const int bh = blockIdx.x / kWgPerHead;
     const int b = bh / Hv, h = bh % Hv, hq = h % Hq;
-    const int tid = threadIdx.x, j = tid & 7;
-    const int col = (blockIdx.x % kWgPerHead) * kCols + (tid >> 3);
+    const int tid = threadIdx.x, j = tid % kLpc;
+    const int col = (blockIdx.x % kWgPerHead) * kCols + tid / kLpc;
     const size_t bt = (size_t)b;  // token index of sequence b (T = 1)
     const size_t vrow = (bt * Hv + h) * kD;
 
     __shared__ half4_t kq_rows[2][kD / 4];
     float4_t* Sc = reinterpret_cast<float4_t*>(state + ((size_t)bh * kD + col) * kD);
-    float4_t s[4];
+    float4_t s[kR];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) s[it] = __builtin_nontemporal_load(Sc + it * 8 + j);
+    for (int it = 0; it < kR; ++it)
+        s[it] = __builtin_nontemporal_load(Sc + it * kLpc + j);
     if (tid < 64) {  // wave 0 -- lanes 0-31: k row, 32-63: q row, 4 halfs each
         const half_t* row = (tid < 32 ? k : q) + (bt * Hq + hq) * kD;
         kq_rows[tid >> 5][tid & 31] = *reinterpret_cast<const half4_t*>(row + 4 * (tid & 31));
@@ -142,10 +159,10 @@ gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
         be = beta[bt * Hv + h];
     }
     __syncthreads();
-    float kr[16], qr[16];
+    float kr[4 * kR], qr[4 * kR];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const half4_t hk = kq_rows[0][it * 8 + j], hq4 = kq_rows[1][it * 8 + j];
+    for (int it = 0; it < kR; ++it) {
+        const half4_t hk = kq_rows[0][it * kLpc + j], hq4 = kq_rows[1][it * kLpc + j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             kr[4 * it + e] = (float)hk[e];
@@ -154,39 +171,39 @@ gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
     }
     float kv = 0.f, sq = 0.f, kq = 0.f;
 #pragma unroll
-    for (int it = 0; it < 4; ++it)
+    for (int it = 0; it < kR; ++it)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             kv = fmaf(s[it][e], kr[4 * it + e], kv);
             sq = fmaf(s[it][e], qr[4 * it + e], sq);
         }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) kq = fmaf(kr[i], qr[i], kq);
-    kv = sum8(kv);
-    sq = sum8(sq);
-    kq = sum8(kq);
+    for (int i = 0; i < 4 * kR; ++i) kq = fmaf(kr[i], qr[i], kq);
+    kv = sum_lanes<kLpc>(kv);
+    sq = sum_lanes<kLpc>(sq);
+    kq = sum_lanes<kLpc>(kq);
     if (kFused) {  // k -> k / max(||k||, eps), q likewise: scale the sums and k itself
         float kk = 0.f, qq = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < 4 * kR; ++i) {
             kk = fmaf(kr[i], kr[i], kk);
             qq = fmaf(qr[i], qr[i], qq);
         }
-        const float kn = 1.f / fmaxf(sqrtf(sum8(kk)), gates.eps);
-        const float qn = 1.f / fmaxf(sqrtf(sum8(qq)), gates.eps);
+        const float kn = 1.f / fmaxf(sqrtf(sum_lanes<kLpc>(kk)), gates.eps);
+        const float qn = 1.f / fmaxf(sqrtf(sum_lanes<kLpc>(qq)), gates.eps);
         kv *= kn;
         sq *= qn;
         kq *= kn * qn;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) kr[i] *= kn;
+        for (int i = 0; i < 4 * kR; ++i) kr[i] *= kn;
     }
     const float d = (vc - g * kv) * be;
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
+    for (int it = 0; it < kR; ++it) {
         float4_t x;
 #pragma unroll
         for (int e = 0; e < 4; ++e) x[e] = fmaf(g, s[it][e], kr[4 * it + e] * d);
-        __builtin_nontemporal_store(x, Sc + it * 8 + j);
+        __builtin_nontemporal_store(x, Sc + it * kLpc + j);
     }
     if (j == 0) out[vrow + col] = (half_t)(scale * fmaf(g, sq, d * kq));
 }
@@ -230,7 +247,7 @@ hipError_t gdn_recurrent(const void* q, const void* k, const void* v, const floa
                          int Hv, float scale, hipStream_t stream) {
     if (T == 1) {
         const unsigned blocks = (unsigned)(B * Hv * (kD / kDecodeCols));
-        hipLaunchKernelGGL((gdn_decode_kernel<kDecodeCols, false>), dim3(blocks), dim3(8 * kDecodeCols),
+        hipLaunchKernelGGL((gdn_decode_kernel<kDecodeCols, kDecodeLpc, false>), dim3(blocks), dim3(kDecodeLpc * kDecodeCols),
                            0, stream, static_cast<const half_t*>(q), static_cast<const half_t*>(k),
                            static_cast<const half_t*>(v), g_log, beta, GdnRawGates{}, state,
                            static_cast<half_t*>(out), Hq, Hv, scale);
@@ -248,7 +265,7 @@ hipError_t gdn_decode_fused(const void* q, const void* k, const void* v, const G
                             float* state, void* out, int B, int Hq, int Hv, float scale,
                             hipStream_t stream) {
     const unsigned blocks = (unsigned)(B * Hv * (kD / kDecodeCols));
-    hipLaunchKernelGGL((gdn_decode_kernel<kDecodeCols, true>), dim3(blocks), dim3(8 * kDecodeCols), 0,
+    hipLaunchKernelGGL((gdn_decode_kernel<kDecodeCols, kDecodeLpc, true>), dim3(blocks), dim3(kDecodeLpc * kDecodeCols), 0,
                        stream, static_cast<const half_t*>(q), static_cast<const half_t*>(k),
                        static_cast<const half_t*>(v), nullptr, nullptr, gates, state,
                        static_cast<half_t*>(out), Hq, Hv, scale);
