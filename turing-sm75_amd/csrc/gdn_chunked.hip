@@ -41,7 +41,6 @@ namespace {
 constexpr int kC = 64;     // chunk
 constexpr int kD = 128;    // dk = dv
 constexpr int kThreads = 256;
-constexpr int kA = 68;     // fp32 row pitch (floats) of the A / Tm tiles: 16-B aligned rows
 constexpr int kStrips = 2; // 16-column strips per carry workgroup
 constexpr int kCarryThreads = 512;  // waves 0-1 chain, 2-3 output, 4-7 DMA
 
@@ -115,18 +114,31 @@ __device__ __forceinline__ void store_dev(float* p, float v) {
 // ----------------------------------------------------------------------------------
 // Prep
 // ----------------------------------------------------------------------------------
+// Packed storage of the ten lower-triangular 16x16 fp32 blocks of a 64 x 64 matrix (A, Tm):
+// block (i, j), j <= i, at (i(i+1)/2 + j) * 256 floats, element (r, c) of a block at
+// 16 r + 4 ((c/4) ^ (r/4 % 4)) + c % 4.  The XOR of 16-byte chunks makes the MFMA operand
+// reads of the block solve (16 rows x 4 columns, 4 rows x 16 columns) hit 64 distinct
+// banks, and keeps 4 consecutive columns in one 16-byte chunk.
+__device__ __forceinline__ int tri_off(int row, int col) {
+    const int i = row >> 4, j = col >> 4, r = row & 15, c = col & 15;
+    return (((i * (i + 1)) >> 1) + j) * 256 + r * 16 + ((((c >> 2) ^ (r >> 2)) & 3) << 2) + (c & 3);
+}
+
+// 37 KB, so four workgroups share a CU.  Region x holds A and Aqk / Tm during the solve,
+// then V for the W / U products, then the U staging; K's region takes the W staging.
 struct PrepLds {
-    half_t K[kC * kD];  // K rows, swizzled
-    union {             // A during the solve; V afterwards; W staging at the end
-        float A[kC][kA];
-        half_t V[kC * kD];
-        half_t Wst[kC * kD];
-    };
-    union {             // Aqk staging first; then Tm; U staging at the end
-        half_t Aqk[kC * kC];
-        float Tm[kC][kA];
-        half_t Ust[kC * kD];
-    };
+    half_t K[kC * kD];          // K rows, swizzled; W staging at the end
+    union {
+        struct {
+            float A[10 * 256];  // strictly lower A, packed blocks
+            union {
+                half_t Aqk[kC * kC];  // Aqk staging
+                float Tm[10 * 256];   // (I + A)^-1, packed blocks
+            };
+        } s;
+        half_t V[kC * kD];      // V rows, swizzled
+        half_t Ust[kC * kD];    // U staging
+    } x;
     float G[kC];
     float bt[kC];
     float bg[kC];
@@ -138,7 +150,7 @@ struct PrepLds {
 // workspace's e^G / e^{G_63 - G}, so the carry multiplies raw K / Q rows by them for free),
 // and g_log / beta are computed from the raw projections a / b (gate arguments).
 template <bool kFused>
-__global__ void __launch_bounds__(kThreads, 3)
+__global__ void __launch_bounds__(kThreads, 4)
 gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
                const half_t* __restrict__ v, const float* __restrict__ g_log,
                const float* __restrict__ beta, GdnRawGates gates, unsigned char* __restrict__ ws,
@@ -227,7 +239,7 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int t = 8 * (r >> 2) + 4 * hi + (r & 3);
-            sm.Aqk[t * kC + perm32(32 + (lane & 31))] = (half_t)0.f;
+            sm.x.s.Aqk[t * kC + perm32(32 + (lane & 31))] = (half_t)0.f;
         }
     } else {
         const int ra = 32 * mt + (lane & 31), rb = 32 * nt + (lane & 31);
@@ -248,11 +260,11 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
             const int t = 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
             const float dec = (rb <= t) ? __expf(sm.G[t] - Gs) : 0.f;
             if (kFused) {
-                if (rb < t) sm.A[t][rb] = sm.bt[t] * kk[r] * (dec * sm.kn[t] * kns);
-                sm.Aqk[t * kC + sp] = (half_t)(qk[r] * (dec * sm.qn[t] * kns));
+                if (rb < t) sm.x.s.A[tri_off(t, rb)] = sm.bt[t] * kk[r] * (dec * sm.kn[t] * kns);
+                sm.x.s.Aqk[t * kC + sp] = (half_t)(qk[r] * (dec * sm.qn[t] * kns));
             } else {
-                if (rb < t) sm.A[t][rb] = sm.bt[t] * kk[r] * dec;
-                sm.Aqk[t * kC + sp] = (half_t)(qk[r] * dec);
+                if (rb < t) sm.x.s.A[tri_off(t, rb)] = sm.bt[t] * kk[r] * dec;
+                sm.x.s.Aqk[t * kC + sp] = (half_t)(qk[r] * dec);
             }
         }
     }
@@ -263,7 +275,7 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int id = it * kThreads + tid;
-        store_dev(wsc + kWsAqk + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.Aqk + id * 8));
+        store_dev(wsc + kWsAqk + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.x.s.Aqk + id * 8));
     }
     if (wave == 1) {
         const float x = sm.G[lane], xc = sm.G[kC - 1];
@@ -283,13 +295,12 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             float acc = (t == cj) ? 1.f : 0.f;
-            const float* arow = &sm.A[16 * bi + t][16 * bi];
 #pragma unroll
-            for (int s = 0; s < t; ++s) acc = fmaf(-arow[s], x[s], acc);
+            for (int s = 0; s < t; ++s) acc = fmaf(-sm.x.s.A[tri_off(16 * bi + t, 16 * bi + s)], x[s], acc);
             x[t] = acc;
         }
 #pragma unroll
-        for (int t = 0; t < 16; ++t) sm.Tm[16 * bi + t][16 * bi + cj] = x[t];
+        for (int t = 0; t < 16; ++t) sm.x.s.Tm[tri_off(16 * bi + t, 16 * bi + cj)] = x[t];
     }
     lds_barrier();
     if (wave < 3) {  // block column j = wave: T_ij = -T_ii X, X = sum_{k=j}^{i-1} A_ik T_kj, i > j
@@ -304,26 +315,21 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
             for (int kb = j; kb < i; ++kb)
 #pragma unroll
                 for (int s4 = 0; s4 < 4; ++s4)
-                    x = mfma16f32(sm.A[16 * i + r16][16 * kb + 4 * s4 + k4],
-                                  sm.Tm[16 * kb + 4 * s4 + k4][16 * j + r16], x);
+                    x = mfma16f32(sm.x.s.A[tri_off(16 * i + r16, 16 * kb + 4 * s4 + k4)],
+                                  sm.x.s.Tm[tri_off(16 * kb + 4 * s4 + k4, 16 * j + r16)], x);
             float4_t t = {};
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4)
-                t = mfma16f32(sm.Tm[16 * i + r16][16 * i + 4 * k4 + s4], x[s4], t);
+                t = mfma16f32(sm.x.s.Tm[tri_off(16 * i + r16, 16 * i + 4 * k4 + s4)], x[s4], t);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sm.Tm[16 * i + 4 * k4 + r][16 * j + r16] = -t[r];
+            for (int r = 0; r < 4; ++r) sm.x.s.Tm[tri_off(16 * i + 4 * k4 + r, 16 * j + r16)] = -t[r];
             wave_lds_sync();
         }
     }
     lds_barrier();
 
-    // ---- 4. V to LDS (over A), then W = Tm diag(beta e^G) K and U = Tm diag(beta) V ----
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int id = it * kThreads + tid;
-        *reinterpret_cast<uint4*>(sm.V + tile_off(id >> 4, id & 15)) = vreg[it];
-    }
-    lds_barrier();
+    // ---- 4. W = Tm diag(beta e^G) K and U = Tm diag(beta) V: the Tm rows become fp16 A
+    // operands in registers, then V goes to LDS over A / Tm ----
     float16_t w_acc[2], u_acc[2];
     {
         const int trow = 32 * mt + (lane & 31);
@@ -333,8 +339,11 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             if (ks >= nks) break;
-            const float4 t0v = *reinterpret_cast<const float4*>(&sm.Tm[trow][16 * ks + 8 * hi]);
-            const float4 t1v = *reinterpret_cast<const float4*>(&sm.Tm[trow][16 * ks + 8 * hi + 4]);
+            // block (trow/16, ks) lies above the diagonal for ks > trow/16: Tm is zero there
+            // and the masked read below goes to a stored block instead
+            const int base = tri_off(trow, 16 * min(ks, trow >> 4) + 8 * hi);
+            const float4 t0v = *reinterpret_cast<const float4*>(&sm.x.s.Tm[base]);
+            const float4 t1v = *reinterpret_cast<const float4*>(&sm.x.s.Tm[base ^ 4]);
             const float tv[8] = {t0v.x, t0v.y, t0v.z, t0v.w, t1v.x, t1v.y, t1v.z, t1v.w};
 #pragma unroll
             for (int qd = 0; qd < 8; ++qd) {
@@ -344,6 +353,13 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
                 au[ks][qd] = (half_t)(x * sm.bt[s]);
             }
         }
+        lds_barrier();
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int id = it * kThreads + tid;
+            *reinterpret_cast<uint4*>(sm.x.V + tile_off(id >> 4, id & 15)) = vreg[it];
+        }
+        lds_barrier();
 #pragma unroll
         for (int n2 = 0; n2 < 2; ++n2) {
             const int ntw = 2 * (wave & 1) + n2;
@@ -355,7 +371,7 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
                 const int row0 = 16 * ks + 8 * hi;
                 const int col0 = 32 * ntw + 16 * (g16 & 1);
                 const half8_t bk = cat8(tile_read_tr(sm.K, row0, col0), tile_read_tr(sm.K, row0 + 4, col0));
-                const half8_t bv = cat8(tile_read_tr(sm.V, row0, col0), tile_read_tr(sm.V, row0 + 4, col0));
+                const half8_t bv = cat8(tile_read_tr(sm.x.V, row0, col0), tile_read_tr(sm.x.V, row0 + 4, col0));
                 w_acc[n2] = mfma32(aw[ks], bk, w_acc[n2]);
                 u_acc[n2] = mfma32(au[ks], bv, u_acc[n2]);
             }
@@ -371,13 +387,13 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int t = 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
-            sm.Wst[t * kD + cp] = (half_t)w_acc[n2][r];
+            sm.K[t * kD + cp] = (half_t)w_acc[n2][r];  // W staging over K
         }
         // U: registers 4a..4a+3 are tokens t0..t0+3 of one column, contiguous in the layout
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
             const int t0 = 32 * mt + 8 * a + 4 * hi;
-            *reinterpret_cast<half4_t*>(&sm.Ust[(((col >> 4) * 4 + (t0 >> 4)) * 64 + ((t0 >> 2) & 3) * 16 + (col & 15)) << 2]) =
+            *reinterpret_cast<half4_t*>(&sm.x.Ust[(((col >> 4) * 4 + (t0 >> 4)) * 64 + ((t0 >> 2) & 3) * 16 + (col & 15)) << 2]) =
                 half4_t{(half_t)u_acc[n2][4 * a], (half_t)u_acc[n2][4 * a + 1], (half_t)u_acc[n2][4 * a + 2],
                         (half_t)u_acc[n2][4 * a + 3]};
         }
@@ -386,8 +402,8 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int id = it * kThreads + tid;
-        store_dev(wsc + kWsW + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.Wst + id * 8));
-        store_dev(wsc + kWsU + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.Ust + id * 8));
+        store_dev(wsc + kWsW + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.K + id * 8));
+        store_dev(wsc + kWsU + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.x.Ust + id * 8));
     }
 
     // ---- 6. publish: every wave's device-scope stores complete, then the chunk's flag ----
