@@ -92,9 +92,12 @@ def test_gdn_chunked_argument_errors():
 
 
 def test_gdn_workspace_bytes_scales_with_chunks():
-    a = tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32)
-    assert tsa.gdn_chunked_workspace_bytes(1, 65, 16, 32) == 2 * a
-    assert tsa.gdn_chunked_workspace_bytes(2, 4096, 16, 32) == 2 * 64 * a
+    # per (sequence, V-head): a 41 984-byte chunk workspace and a 4-byte ready flag per chunk,
+    # and a 4-byte abort word for each of the 4 carry workgroups (32 state columns each)
+    per_head = lambda nch: nch * (41984 + 4) + 4 * 4
+    assert tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32) == 32 * per_head(1)
+    assert tsa.gdn_chunked_workspace_bytes(1, 65, 16, 32) == 32 * per_head(2)
+    assert tsa.gdn_chunked_workspace_bytes(2, 4096, 16, 32) == 2 * 32 * per_head(64)
     assert tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32, dk=64) == 0
     assert tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32, chunk=32) == 0
 

@@ -6,6 +6,8 @@ Gates: outputs max-abs < 0.02 (fp16 I/O, src/gdn_sm75.cu:1313) and the fp32 stat
 Cases: float64 fixtures; the T=4096, Hq=16, Hv=32, C=64 prefill in full; the
 reference driver's LCG inputs and shape (Hv=48, T=512); ragged T and head maps with
 Hv % Hq != 0; batches; state continuity across calls (prefill -> prefill -> decode); the
+chunked carry giving up on unready chunks (forced, and under serialised dispatch) and the
+second launch redoing it; the
 decode step of 16 sequences x 32 heads (N(0, 0.02) state) over 64 steps in full and 512 steps
 on a subset of sequences.
 """
@@ -179,3 +181,60 @@ def test_workspace_too_small_raises(dev):
     with pytest.raises(tsa.TsaError) as e:
         tsa.gdn_chunked_fwd(q, k, v, g, beta, st, ws=ws)
     assert e.value.code == tsa.TSA_ERR_WORKSPACE
+
+
+def test_chunked_carry_gives_up_and_is_redone(dev, orc, monkeypatch):
+    """Beside the prep, a carry workgroup that finds a chunk not ready gives up (wait limit 0
+    through TSA_GDN_CARRY_WAIT_US), leaves its state columns alone, and the second carry launch
+    after the prep redoes it.  Whatever mix of workgroups gives up, the results equal the
+    default run bit for bit and the oracle within the gates."""
+    rng = np.random.default_rng(402)
+    q, k, v, g, beta, st = _inputs(rng, 1, 1024, 16, 32, sstd=0.02)
+    o0, s0 = _gpu(dev, "chunked", q, k, v, g, beta, st)
+    monkeypatch.setenv("TSA_GDN_CARRY_WAIT_US", "0")
+    for _ in range(3):
+        o1, s1 = _gpu(dev, "chunked", q, k, v, g, beta, st)
+        assert np.array_equal(o1, o0) and np.array_equal(s1, s0)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    _check(o1, s1, o_ref, s_ref, *TOL["chunked"], label="chunked, carry waits limited to 0")
+
+
+_SERIAL_CHILD = r"""
+import sys
+import numpy as np
+import torch
+sys.path[:0] = sys.argv[1:3]
+import oracle, tsa
+rng = np.random.default_rng(403)
+B, T, Hq, Hv, D = 1, 768, 16, 32, 128
+l2n = lambda x: x / np.linalg.norm(x, axis=-1, keepdims=True)
+q = l2n(rng.standard_normal((B, T, Hq, D))).astype(np.float16)
+k = l2n(rng.standard_normal((B, T, Hq, D))).astype(np.float16)
+v = rng.standard_normal((B, T, Hv, D)).astype(np.float16)
+beta = (1 / (1 + np.exp(-rng.standard_normal((B, T, Hv))))).astype(np.float32)
+g = (-np.logaddexp(0.0, rng.standard_normal((B, T, Hv)))).astype(np.float32)
+st = (0.02 * rng.standard_normal((B, Hv, D, D))).astype(np.float32)
+dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+ts = dv(st)
+o = tsa.gdn_chunked_fwd(dv(q), dv(k), dv(v), dv(g), dv(beta), ts).float().cpu().numpy()
+o_ref, s_ref = oracle.gdn_serial(q, k, v, g, beta, st)
+eo = float(np.abs(o - o_ref).max())
+es = float(np.abs(ts.cpu().numpy() - s_ref).max() / np.abs(s_ref).max())
+print(f"serialised dispatch: out max-abs {eo:.2e} state rel {es:.2e}", flush=True)
+sys.exit(0 if (eo < 2e-3 and es < 8e-4) else 1)
+"""
+
+
+def test_chunked_under_serialised_dispatch(dev):
+    """With every dispatch serialised (AMD_SERIALIZE_KERNEL=3, as under a profiler that
+    collects counters), the carry launched beside the prep cannot see it run; it must give up,
+    and the second launch must still produce the correct result (one child process)."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, AMD_SERIALIZE_KERNEL="3")
+    r = subprocess.run([sys.executable, "-c", _SERIAL_CHILD, root, os.path.join(root, "turing-sm75_amd")],
+                       env=env, capture_output=True, text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0

@@ -28,6 +28,7 @@
 //   register holds prefetched data and each wave reads its MFMA operands from LDS in
 //   batches ahead of the MFMAs.
 #include <atomic>
+#include <cstdlib>
 #include <mutex>
 #include <random>
 #include <type_traits>
@@ -57,9 +58,21 @@ constexpr int kWsChunk = kWsG + kC * 16;    // 41984 B, multiple of 256
 // call's epoch there once the chunk's workspace is in memory; the carry's DMA waves wait
 // for it before copying the chunk.  Epochs differ from call to call, so flags left by an
 // earlier call never read as ready and nothing has to clear them.
-// A wait gives up after kSpinMax polls (a few tenths of a second) and the carry then
-// writes NaN state instead of hanging.
-constexpr int kSpinMax = 1 << 18;
+// A wait gives up after a limit on the 100 MHz real-time counter (2 ms; the environment
+// variable TSA_GDN_CARRY_WAIT_US sets it in microseconds, 0 = give up whenever a chunk is
+// not ready at the first look, which is how the tests exercise the path).  When the prep
+// runs beside the carry, a workgroup that gave up leaves its state columns untouched and
+// writes the call's epoch to its abort word (after the ready flags, one per carry
+// workgroup); a second launch of the carry, ordered after the prep on the caller's stream,
+// runs exactly the workgroups whose abort word holds the epoch and exits at once in the
+// others.  Waits time out when the two kernels do not run at the same time: a profiler or a
+// runtime setting that serialises dispatches, or a device busy with other work.  A wait
+// that times out where no second launch follows poisons the state with NaN.
+
+// Carry launch modes.
+constexpr int kCarryInOrder = 0;  // after the prep on one stream: waits never block
+constexpr int kCarryBeside = 1;   // beside the prep: a timed-out workgroup aborts
+constexpr int kCarryRetry = 2;    // after the prep: only the aborted workgroups run
 
 // Within each aligned 32-block, index 16a + 4g + b is stored at 8g + 4a + b.  A 16x16x32
 // MFMA lane of group g then finds its 8 k-values {16a + 4g + b} in one 16-byte run; that
@@ -513,8 +526,8 @@ __device__ __forceinline__ void dma_wait_barrier() {
 template <int W>
 __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const unsigned char* kh,
                                          const unsigned char* qh, const unsigned char* wsh,
-                                         const unsigned* fl, unsigned epoch, int* err,
-                                         unsigned rowbytes, int pair, int T, int nch) {
+                                         const unsigned* fl, unsigned epoch, unsigned wait_ticks,
+                                         int* err, unsigned rowbytes, int pair, int T, int nch) {
     constexpr int kJ = (kDmaN - W + 3) / 4;
     const int lane = threadIdx.x & 63;
     unsigned off[kJ];
@@ -552,16 +565,20 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
     // fl[n] is chunk n's flag (device-scope loads, like the workspace copies that follow
     // it).  The flag of the next chunk is loaded right after a chunk's copies are issued, so
     // its round trip overlaps them and a chunk that is ready costs no wait.  After one
-    // timed-out wait, no more waits.
+    // timed-out wait, no more waits (the workgroup's results are then discarded).
     auto peek = [&](int n) -> unsigned {
         return n < nch ? __hip_atomic_load(fl + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
     };
+    // real-time counter (100 MHz), low 32 bits; readfirstlane keeps the wait loop uniform
+    auto now = []() { return __builtin_amdgcn_readfirstlane((unsigned)__builtin_amdgcn_s_memrealtime()); };
     auto ready = [&](int n, unsigned v) {
         v = __builtin_amdgcn_readfirstlane(v);
-        for (int s = 0; v != epoch && !*err; ++s) {
-            if (s == kSpinMax) {
+        if (v == epoch || *err) return;
+        const unsigned t0 = now();
+        while (v != epoch) {
+            if (now() - t0 >= wait_ticks) {
                 *err = 1;
-                break;
+                return;
             }
             __builtin_amdgcn_s_sleep(8);
             v = __builtin_amdgcn_readfirstlane(
@@ -753,9 +770,14 @@ __device__ __forceinline__ void out_flush(const half_t* ostage, half_t* out, int
 __global__ void __launch_bounds__(kCarryThreads, 1)
 gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
                 const unsigned char* __restrict__ ws, const unsigned* __restrict__ flags,
-                unsigned epoch, float* __restrict__ state, half_t* __restrict__ out, int T, int Hq, int Hv,
-                int nch, int BHv, float scale) {
+                unsigned* __restrict__ aborts, unsigned epoch, int mode, unsigned wait_ticks,
+                float* __restrict__ state,
+                half_t* __restrict__ out, int T, int Hq, int Hv, int nch, int BHv, float scale) {
     __shared__ CarryLds sm;
+    if (mode == kCarryRetry &&
+        __builtin_amdgcn_readfirstlane(__hip_atomic_load(aborts + blockIdx.x, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT)) != epoch)
+        return;  // this workgroup finished in the launch beside the prep
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: role branches are scalar
     const int g = lane >> 4, c = lane & 15;
@@ -816,20 +838,28 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
         const unsigned* fl = flags + (size_t)bh * nch;
         int* err = &sm.err[wave - 4];
         switch (wave) {
-            case 4: dma_role<0>(slot_lds, kh, qh, wsh, fl, epoch, err, rowbytes, pair, T, nch); break;
-            case 5: dma_role<1>(slot_lds, kh, qh, wsh, fl, epoch, err, rowbytes, pair, T, nch); break;
-            case 6: dma_role<2>(slot_lds, kh, qh, wsh, fl, epoch, err, rowbytes, pair, T, nch); break;
-            default: dma_role<3>(slot_lds, kh, qh, wsh, fl, epoch, err, rowbytes, pair, T, nch); break;
+            case 4: dma_role<0>(slot_lds, kh, qh, wsh, fl, epoch, wait_ticks, err, rowbytes, pair, T, nch); break;
+            case 5: dma_role<1>(slot_lds, kh, qh, wsh, fl, epoch, wait_ticks, err, rowbytes, pair, T, nch); break;
+            case 6: dma_role<2>(slot_lds, kh, qh, wsh, fl, epoch, wait_ticks, err, rowbytes, pair, T, nch); break;
+            default: dma_role<3>(slot_lds, kh, qh, wsh, fl, epoch, wait_ticks, err, rowbytes, pair, T, nch); break;
         }
     }
     if (chain) {
-        // a timed-out wait means the chunk operands were never published: poison the state
+        // a timed-out wait means some chunk operands were read before they were published:
+        // beside the prep, leave the state for the second launch; otherwise poison it
         const bool lost = (sm.err[0] | sm.err[1] | sm.err[2] | sm.err[3]) != 0;
-        const float nan = __builtin_nanf("");
+        // the abort word is written by every launch beside the prep (epoch or 0), so a value
+        // left by an earlier call never sends a finished workgroup into the second launch
+        if (mode == kCarryBeside && tid == 0)
+            __hip_atomic_store(aborts + blockIdx.x, lost ? epoch : 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        if (!(lost && mode == kCarryBeside)) {
+            const float nan = __builtin_nanf("");
 #pragma unroll
-        for (int m = 0; m < 8; ++m)
-            *reinterpret_cast<float4*>(Sg + 16 * m + 4 * g) =
-                lost ? make_float4(nan, nan, nan, nan) : make_float4(S[m][0], S[m][1], S[m][2], S[m][3]);
+            for (int m = 0; m < 8; ++m)
+                *reinterpret_cast<float4*>(Sg + 16 * m + 4 * g) =
+                    lost ? make_float4(nan, nan, nan, nan) : make_float4(S[m][0], S[m][1], S[m][2], S[m][3]);
+        }
     } else if (outw) {
         out_flush(sm.OS[wave - 2], out, b, T, Hv, h, (nch - 1) * kC, pair, wave - 2);
     }
@@ -839,7 +869,9 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
 
 size_t gdn_chunked_ws_bytes(int B, int T, int Hv) {
     const size_t nch = (size_t)(T + kC - 1) / kC;
-    return (size_t)B * Hv * nch * (kWsChunk + sizeof(unsigned));
+    // chunk workspaces, then a ready flag per chunk, then an abort word per carry workgroup
+    return (size_t)B * Hv * nch * (kWsChunk + sizeof(unsigned)) +
+           (size_t)B * Hv * (kD / (16 * kStrips)) * sizeof(unsigned);
 }
 
 namespace {
@@ -866,6 +898,18 @@ unsigned next_epoch() {
     return e ? e : ++counter;
 }
 
+// Longest wait of a carry workgroup for a chunk, in ticks of the 100 MHz real-time counter.
+unsigned carry_wait_ticks() {
+    const char* e = std::getenv("TSA_GDN_CARRY_WAIT_US");
+    long us = 2000;
+    if (e && *e) {
+        char* end = nullptr;
+        const long v = std::strtol(e, &end, 10);
+        if (end && *end == 0 && v >= 0 && v <= 10000000) us = v;
+    }
+    return (unsigned)(us * 100);
+}
+
 template <bool kFused>
 hipError_t launch_chunked(const void* q, const void* k, const void* v, const float* g_log,
                           const float* beta, const GdnRawGates& gates, float* state, void* out,
@@ -877,17 +921,19 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
     auto K = static_cast<const half_t*>(k);
     auto W = static_cast<unsigned char*>(ws);
     unsigned* flags = reinterpret_cast<unsigned*>(W + (size_t)BHv * nch * kWsChunk);
+    unsigned* aborts = flags + (size_t)BHv * nch;
     const unsigned epoch = next_epoch();
+    const unsigned wait_ticks = carry_wait_ticks();
     auto prep = [&](hipStream_t st) {
         hipLaunchKernelGGL(gdn_chunk_prep<kFused>, dim3(BHv * nch), dim3(kThreads), 0, st, Q, K,
                            static_cast<const half_t*>(v), g_log, beta, gates, W, flags, epoch, T,
                            Hq, Hv, nch, BHv);
         return hipGetLastError();
     };
-    auto carry = [&]() {
+    auto carry = [&](int mode) {
         hipLaunchKernelGGL(gdn_chunk_carry, dim3(carry_wgs), dim3(kCarryThreads), 0, stream, Q, K, W,
-                           flags, epoch, state, static_cast<half_t*>(out), T, Hq, Hv, nch, BHv,
-                           scale);
+                           flags, aborts, epoch, mode, wait_ticks, state, static_cast<half_t*>(out), T,
+                           Hq, Hv, nch, BHv, scale);
         return hipGetLastError();
     };
 
@@ -913,18 +959,20 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
     }
     if (!side) {
         hipError_t e = prep(stream);
-        return e != hipSuccess ? e : carry();
+        return e != hipSuccess ? e : carry(kCarryInOrder);
     }
     // fork: the prep starts after the caller's earlier work; the carry is queued first so its
     // workgroups take their CUs before the prep fills the rest; join: later work on the
-    // caller's stream (and the next call's prep) waits for this prep.
+    // caller's stream (and the next call's prep) waits for this prep; then the second carry
+    // launch, which redoes any workgroup that gave up waiting (and otherwise exits at once).
     std::lock_guard<std::mutex> lock(g_side_mu);
     hipError_t e = hipEventRecord(side->fork, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(side->s, side->fork, 0);
-    if (e == hipSuccess) e = carry();
+    if (e == hipSuccess) e = carry(kCarryBeside);
     if (e == hipSuccess) e = prep(side->s);
     if (e == hipSuccess) e = hipEventRecord(side->join, side->s);
     if (e == hipSuccess) e = hipStreamWaitEvent(stream, side->join, 0);
+    if (e == hipSuccess) e = carry(kCarryRetry);
     return e;
 }
 }  // namespace
