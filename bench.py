@@ -246,7 +246,7 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=512,
                     help="length of the extra decode-only run (the 512-step workload)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
-                    help="after the measurements, run one plain device copy of this many MiB "
+                    help="after the measurements, run one plain copy kernel over this many MiB "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -387,7 +387,7 @@ def main():
         src = torch.ones(n_el, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
-        dst.copy_(src)
+        torch.mul(src, 1.0, out=dst)  # one elementwise copy kernel (a device copy may use DMA)
         torch.cuda.synchronize()
         del src, dst
 
