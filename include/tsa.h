@@ -44,8 +44,8 @@ const char* tsa_strerror(int code);
 const char* tsa_version(void);
 
 /* Softmax flash-attention forward, O = softmax(scale * Q K^T [+ causal mask]) V.
- * Replaces launch_wmma<D> / launch_ffma<D> (src/attn_sm75.cu:421-440, dispatched on D at
- * :481-488) and its kernel flash_attn_sm75_wmma (:239-375).  D in {64, 128} as the
+ * Replaces launch_wmma<D> (src/attn_sm75.cu:432-440, dispatched on D at :481-484) and its
+ * kernel flash_attn_sm75_wmma (:239-375).  D in {64, 128} as the
  * reference, and 256; any S >= 1 (the reference caps S at 1024 for its naive check only,
  * :457-460); causal 0 or 1 (the reference hard-codes 1, :463).  fp32 softmax statistics,
  * fp16 MFMA. */
@@ -58,6 +58,13 @@ int tsa_attn_fwd(const void* q, const void* k, const void* v, void* o, int B, in
  * its S <= 1024 threads-per-block limit.  Used by the attn_sm75 driver's error check. */
 int tsa_attn_naive(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
                    int D, float scale, int causal, void* stream);
+
+/* The same attention forward on the vector ALUs only (fp32 FMA dots, no MFMA): the
+ * same-binary opponent of tsa_attn_fwd, as launch_ffma<D> / flash_attn_sm75_ffma
+ * (src/attn_sm75.cu:421-430, :107-233) is of the WMMA kernel in the reference's driver.
+ * Same arguments, layouts, shapes and error codes as tsa_attn_fwd. */
+int tsa_attn_fwd_valu(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
+                      int D, float scale, int causal, void* stream);
 
 /* Gated grouped-query attention: O = softmax(scale * Q K^T [+ causal mask]) V, then
  * O *= sigmoid(gate) element-wise when gate is not NULL.  The attention layer of the

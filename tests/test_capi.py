@@ -55,6 +55,16 @@ def test_attn_argument_errors():
     assert lib.tsa_attn_naive(DUMMY, DUMMY, NULL, DUMMY, 1, 1, 4, 64, 0.1, 0, NULL) == tsa.TSA_ERR_NULL
 
 
+def test_attn_valu_argument_errors():
+    # the VALU opponent validates exactly as tsa_attn_fwd
+    f = tsa.load().tsa_attn_fwd_valu
+    assert f(DUMMY, NULL, DUMMY, DUMMY, 1, 1, 16, 128, 0.1, 1, NULL) == tsa.TSA_ERR_NULL
+    assert f(DUMMY, DUMMY, DUMMY, DUMMY, 1, 1, 0, 128, 0.1, 1, NULL) == tsa.TSA_ERR_SHAPE
+    assert f(DUMMY, DUMMY, DUMMY, DUMMY, 1, 1, 16, 96, 0.1, 1, NULL) == tsa.TSA_ERR_UNSUPPORTED
+    assert f(DUMMY, DUMMY, DUMMY, DUMMY, 1, 1, 16, 64, 0.1, 3, NULL) == tsa.TSA_ERR_ARG
+    assert f(DUMMY, DUMMY, DUMMY, DUMMY, 1, 1, 16, 64, float("inf"), 0, NULL) == tsa.TSA_ERR_ARG
+
+
 def _gqa(*, q=DUMMY, gate=NULL, B=1, Hq=24, Hkv=4, S=16, D=256, scale=0.1, causal=1):
     return tsa.load().tsa_attn_gqa_fwd(q, DUMMY, DUMMY, gate, DUMMY, B, Hq, Hkv, S, D, scale,
                                        causal, NULL)

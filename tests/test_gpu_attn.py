@@ -1,4 +1,5 @@
-"""GPU parity: the MFMA flash-attention kernel (tsa_attn_fwd) against the CPU oracle.
+"""GPU parity: the MFMA flash-attention kernel (tsa_attn_fwd) and its VALU opponent
+(tsa_attn_fwd_valu) against the CPU oracle.
 
 Gate: max-abs error < 0.02 on fp16 outputs (the reference's gate, src/attn_sm75.cu:501-502);
 a tighter 5e-3 bound guards against regressions that the gate would still let through.
@@ -6,7 +7,8 @@ Cases: the float64 fixtures, B=1 H=4 S=256 D=128 non-causal, B=2 H=8 S=512 causa
 128, B=1 H=32 S=8192 D=128 causal with outliers (against a seeded sample of oracle rows plus
 the full on-device naive kernel), the reference's own inputs
 (mt19937(42), N(0, 0.5), src/attn_sm75.cu:398,473-476), ragged S, and size-independent
-properties at full size (row 0 of a causal head is V[0] exactly).
+properties at full size (row 0 of a causal head is V[0] exactly).  The VALU kernel runs the
+fixtures, the first two shapes at every D, ragged S and the reference's inputs.
 """
 import numpy as np
 import pytest
@@ -23,10 +25,10 @@ def _to_dev(dev, *arrays):
     return [torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in arrays]
 
 
-def _run(dev, q, k, v, causal, naive=False):
+def _run(dev, q, k, v, causal, naive=False, valu=False):
     import torch
     tq, tk, tv = _to_dev(dev, q, k, v)
-    o = tsa.attn_fwd(tq, tk, tv, causal=causal, naive=naive)
+    o = tsa.attn_fwd(tq, tk, tv, causal=causal, naive=naive, valu=valu)
     torch.cuda.synchronize()
     return o.cpu().numpy()
 
@@ -205,3 +207,42 @@ def test_gated_gqa_target_layer(dev, orc):
     e_orc = _err(o.cpu().numpy().reshape(-1, D)[rows], ref)
     print(f"gated GQA 24/4 D=256 S=8192: max-abs vs naive kernel {e_naive:.5f}, vs oracle rows {e_orc:.5f}")
     assert e_orc < TIGHT and e_naive < GATE
+
+
+# ---- the VALU opponent (no MFMA): same recurrence, fp32 FMA dots ----
+@pytest.mark.parametrize("i", range(4))
+def test_valu_golden_fixtures(dev, golden, i):
+    g = golden("attn_golden.npz")
+    B, H, S, D, causal = (int(x) for x in g[f"c{i}_meta"])
+    o = _run(dev, g[f"c{i}_q"], g[f"c{i}_k"], g[f"c{i}_v"], bool(causal), valu=True)
+    assert _err(o, g[f"c{i}_o"]) < TIGHT
+
+
+@pytest.mark.parametrize("shape,causal", [((1, 4, 256, 128), False), ((2, 8, 512, 64), True),
+                                          ((2, 8, 512, 128), True), ((1, 2, 300, 256), True),
+                                          ((1, 2, 200, 256), False)])
+def test_valu_shapes(dev, orc, shape, causal):
+    rng = np.random.default_rng(150 + shape[2] + shape[3])
+    q, k, v = (_normal(rng, shape) for _ in range(3))
+    ref = orc.attn_naive(q, k, v, causal)
+    ev = _err(_run(dev, q, k, v, causal, valu=True), ref)
+    em = _err(_run(dev, q, k, v, causal), ref)
+    print(f"{shape} causal={causal}: valu max-abs {ev:.5f}, mfma {em:.5f}")
+    assert ev < TIGHT
+
+
+@pytest.mark.parametrize("S", [1, 2, 63, 64, 65, 129])
+@pytest.mark.parametrize("causal", [False, True])
+def test_valu_ragged(dev, orc, S, causal):
+    rng = np.random.default_rng(170 + S)
+    q, k, v = (_normal(rng, (1, 3, S, 64)) for _ in range(3))
+    assert _err(_run(dev, q, k, v, causal, valu=True), orc.attn_naive(q, k, v, causal)) < TIGHT
+
+
+def test_valu_reference_driver_inputs(dev, orc):
+    # the reference's own inputs: mt19937(42), N(0, 0.5) -> fp16 for Q, K, V in that order
+    shape = (2, 8, 512, 128)
+    n = int(np.prod(shape))
+    qkv = orc.mt_normal_half(42, 0.0, 0.5, n, 3).view(np.float16).reshape((3,) + shape)
+    q, k, v = qkv[0], qkv[1], qkv[2]
+    assert _err(_run(dev, q, k, v, True, valu=True), orc.attn_naive(q, k, v, True)) < TIGHT

@@ -30,7 +30,8 @@ int check_attn(const void* q, const void* k, const void* v, const void* o, int B
     // The running max is taken over raw q.k, which is the max of the scaled scores only
     // for scale > 0 (the reference's scale is 1/sqrt(D), src/attn_sm75.cu:462).
     if (!(scale > 0.f) || !std::isfinite(scale)) return TSA_ERR_ARG;
-    // workgroups: B*H*ceil(S/128) for the MFMA kernel, B*H*S/128 for the naive one
+    // workgroups: B*H*ceil(S/128) for the MFMA kernel, B*H*ceil(S/64) for the VALU one,
+    // B*H*S/128 for the naive one
     if (!fits_int(B, H, S)) return TSA_ERR_SHAPE;
     return TSA_OK;
 }
@@ -84,6 +85,13 @@ extern "C" int tsa_attn_naive(const void* q, const void* k, const void* v, void*
     if (rc) return rc;
     return from_hip(tsa::attn_naive(q, k, v, nullptr, o, B, H, H, S, D, scale, causal,
                                     as_stream(stream)));
+}
+
+extern "C" int tsa_attn_fwd_valu(const void* q, const void* k, const void* v, void* o, int B,
+                                 int H, int S, int D, float scale, int causal, void* stream) {
+    const int rc = check_attn(q, k, v, o, B, H, S, D, scale, causal);
+    if (rc) return rc;
+    return from_hip(tsa::attn_valu(q, k, v, o, B, H, S, D, scale, causal, as_stream(stream)));
 }
 
 extern "C" int tsa_attn_gqa_fwd(const void* q, const void* k, const void* v, const void* gate,

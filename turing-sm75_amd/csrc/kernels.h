@@ -12,6 +12,9 @@ hipError_t attn_fwd(const void* q, const void* k, const void* v, const void* gat
 hipError_t attn_naive(const void* q, const void* k, const void* v, const void* gate, void* o,
                       int B, int Hq, int Hkv, int S, int D, float scale, int causal,
                       hipStream_t stream);
+// The VALU opponent (no MFMA): q, k, v, o [B][H][S][D].
+hipError_t attn_valu(const void* q, const void* k, const void* v, void* o, int B, int H, int S,
+                     int D, float scale, int causal, hipStream_t stream);
 
 // Raw inputs of the fused pre-ops (the target model's layer): a, b [B][T][Hv]; dt_bias, A
 // [Hv] (A = -exp(A_log)); eps of the q / k l2 norms.  g_log = softplus(a + dt_bias) * A,

@@ -8,7 +8,9 @@
 // normal_distribution(0, std) rounded to fp16 for Q, K, V in that order (seed 42, std 0.5 as
 // in :398,473-476), the MFMA kernel checked against the naive kernel by max-abs error with
 // the 0.02 gate, 20 timed iterations, TFLOP/s in the dense-equivalent (4 B H S^2 D) and
-// causal-executed (2 B H S (S+1) D) conventions (:531-535), exit 0 iff the check passes.
+// causal-executed (2 B H S (S+1) D) conventions (:531-535), exit 0 iff the MFMA kernel's
+// check passes.  The VALU kernel (tsa_attn_fwd_valu) is checked and timed beside it for plain
+// attention, as the reference's FFMA kernel is (:486-489,500-502,521-528).
 // Differences: causal is a flag (the reference hard-codes 1, :463) and S is not capped at
 // 1024 (the naive check here is O(S^2 D), not O(S^2 D^2)).  --outlier P multiplies each
 // element by 8 with probability P (independent mt19937(seed + 1) stream).  D = 256 is
@@ -76,6 +78,7 @@ int main(int argc, char** argv) {
         for (size_t i = 0; i < hg.size(); ++i) hg[i] = (f16)gd(rng);
     }
     DevBuf<f16> Q(elems), K(kv_elems), V(kv_elems), G(gated ? elems : 1), Om(elems), On(elems);
+    DevBuf<f16> Of(gated || Hkv != H ? 1 : elems);
     Q.upload(hq);
     K.upload(hk);
     V.upload(hv);
@@ -86,25 +89,39 @@ int main(int argc, char** argv) {
         if (gqa) DRV_TSA(tsa_attn_gqa_fwd(Q.d, K.d, V.d, gp, Om.d, B, H, Hkv, S, D, scale, causal, nullptr));
         else DRV_TSA(tsa_attn_fwd(Q.d, K.d, V.d, Om.d, B, H, S, D, scale, causal, nullptr));
     };
+    // the VALU opponent (no MFMA), as the reference's launch_ffma (src/attn_sm75.cu:486-489);
+    // plain attention only (the reference's lab has no grouped-query or gated variant)
+    auto run_valu = [&] { DRV_TSA(tsa_attn_fwd_valu(Q.d, K.d, V.d, Of.d, B, H, S, D, scale, causal, nullptr)); };
     auto run_naive = [&] {
         if (gqa) DRV_TSA(tsa_attn_gqa_naive(Q.d, K.d, V.d, gp, On.d, B, H, Hkv, S, D, scale, causal, nullptr));
         else DRV_TSA(tsa_attn_naive(Q.d, K.d, V.d, On.d, B, H, S, D, scale, causal, nullptr));
     };
 
     run_mfma();
+    if (!gqa) run_valu();
     run_naive();
     DRV_HIP(hipDeviceSynchronize());
-    std::vector<f16> om, on;
+    std::vector<f16> om, on, of;
     Om.download(om);
     On.download(on);
-    float err = 0.f;
-    for (size_t i = 0; i < elems; ++i) {
-        const float d = std::fabs((float)om[i] - (float)on[i]);
-        err = (d > err || d != d) ? d : err;
-    }
+    auto max_err = [&](const std::vector<f16>& a) {
+        float e = 0.f;
+        for (size_t i = 0; i < elems; ++i) {
+            const float d = std::fabs((float)a[i] - (float)on[i]);
+            e = (d > e || d != d) ? d : e;
+        }
+        return e;
+    };
+    const float err = max_err(om);
     std::printf("max |mfma-naive| : %.5f   %s\n", err, err < 2e-2f ? "OK" : "FAIL");
+    if (!gqa) {
+        Of.download(of);
+        const float err_v = max_err(of);
+        std::printf("max |valu-naive| : %.5f   %s\n", err_v, err_v < 2e-2f ? "OK" : "FAIL");
+    }
 
     const float mfma_ms = time_ms(run_mfma, iters);
+    const float valu_ms = gqa ? 0.f : time_ms(run_valu, iters);
     const int naive_iters = S > 2048 ? 1 : iters;
     const float naive_ms = time_ms(run_naive, naive_iters);
 
@@ -114,7 +131,12 @@ int main(int argc, char** argv) {
     std::printf("mfma  (gfx950)  : %8.4f ms   %7.1f TFLOP/s dense-eq   %7.1f %s\n", mfma_ms,
                 tflops(flops_dense, mfma_ms), tflops(flops_exec, mfma_ms),
                 causal ? "causal-exec" : "executed");
+    if (!gqa)
+        std::printf("valu  (gfx950)  : %8.4f ms   %7.1f TFLOP/s dense-eq   %7.1f %s\n", valu_ms,
+                    tflops(flops_dense, valu_ms), tflops(flops_exec, valu_ms),
+                    causal ? "causal-exec" : "executed");
     std::printf("naive oracle    : %8.4f ms   (not a realistic fallback)\n", naive_ms);
+    if (!gqa) std::printf("mfma vs valu    : %.2fx  (same FLOP convention both sides)\n", valu_ms / mfma_ms);
     std::printf("mfma vs naive   : %.2fx\n", naive_ms / mfma_ms);
     return err < 2e-2f ? 0 : 1;
 }

@@ -50,6 +50,7 @@ _SIGNATURES = {
     "tsa_version": (ctypes.c_char_p, []),
     "tsa_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp]),
     "tsa_attn_naive": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp]),
+    "tsa_attn_fwd_valu": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp]),
     "tsa_attn_gqa_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp]),
     "tsa_attn_gqa_naive": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp]),
     "tsa_gdn_chunked_workspace_bytes": (_sz, [_i] * 7),
@@ -131,8 +132,9 @@ def _ptr(t):
 # ---------------------------------------------------------------------------------------
 # attention
 # ---------------------------------------------------------------------------------------
-def attn_fwd(q, k, v, out=None, scale=None, causal=True, stream=None, naive=False):
-    """O = softmax(scale Q K^T [+ causal mask]) V on the MFMA kernel (or the naive one)."""
+def attn_fwd(q, k, v, out=None, scale=None, causal=True, stream=None, naive=False, valu=False):
+    """O = softmax(scale Q K^T [+ causal mask]) V on the MFMA kernel (or the naive one, or the
+    VALU opponent with valu=True)."""
     import torch
     for name, t in (("q", q), ("k", k), ("v", v)):
         _need(t, torch.float16, 4, name)
@@ -146,7 +148,9 @@ def attn_fwd(q, k, v, out=None, scale=None, causal=True, stream=None, naive=Fals
         raise ValueError("out shape differs from q")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    fn = load().tsa_attn_naive if naive else load().tsa_attn_fwd
+    if naive and valu:
+        raise ValueError("naive and valu select different kernels")
+    fn = load().tsa_attn_naive if naive else (load().tsa_attn_fwd_valu if valu else load().tsa_attn_fwd)
     _check(fn(_ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, S, D, float(scale), int(bool(causal)),
               _stream(stream)))
     return out
