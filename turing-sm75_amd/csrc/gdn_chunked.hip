@@ -945,18 +945,25 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
     // kernels in order (a graph does not promise to run sibling nodes concurrently).
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
+    // The side stream belongs to the device of the caller's stream (the null stream: the
+    // current device), which need not be the current device.
     int dev = -1;
+    const bool have_dev = stream ? hipStreamGetDevice(stream, &dev) == hipSuccess
+                                 : hipGetDevice(&dev) == hipSuccess;
     SideStream* side = nullptr;
-    if (cap == hipStreamCaptureStatusNone && hipGetDevice(&dev) == hipSuccess && dev >= 0 &&
-        dev < kMaxDevices) {
+    if (cap == hipStreamCaptureStatusNone && have_dev && dev >= 0 && dev < kMaxDevices) {
         std::lock_guard<std::mutex> lock(g_side_mu);
         SideStream& d = g_side[dev];
-        if (!d.tried) {
+        if (!d.tried) {  // create the stream and events on that device
             d.tried = true;
-            d.ok = hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            int cur = -1;
+            const bool switched = hipGetDevice(&cur) == hipSuccess && cur != dev && hipSetDevice(dev) == hipSuccess;
+            d.ok = (cur == dev || switched) &&
+                   hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
                    hipStreamCreateWithFlags(&d.s, hipStreamNonBlocking) == hipSuccess &&
                    hipEventCreateWithFlags(&d.fork, hipEventDisableTiming) == hipSuccess &&
                    hipEventCreateWithFlags(&d.join, hipEventDisableTiming) == hipSuccess;
+            if (switched) (void)hipSetDevice(cur);
         }
         if (d.ok && 2 * carry_wgs <= d.cus && nch > 1) side = &d;
     }
