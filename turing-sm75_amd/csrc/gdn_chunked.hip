@@ -63,19 +63,20 @@ constexpr int kWsChunk = kWsG + kC * 16;    // 41984 B, multiple of 256
 // not ready at the first look, which is how the tests exercise the path).  When the prep
 // runs beside the carry, a workgroup that gave up leaves its state columns untouched and
 // writes the call's epoch to its abort word (after the ready flags, one per carry
-// workgroup); a second launch of the carry, right after the first on the caller's stream,
-// runs exactly the workgroups whose abort word holds the epoch (waiting for the prep's
-// flags, up to 1 s) and exits at once in the others.  Waits time out when the two kernels do not run at the same time: a profiler or a
+// workgroup); a second launch of the carry, ordered after the prep on the caller's stream,
+// runs exactly the workgroups whose abort word holds the epoch and exits at once in the
+// others.  Waits time out when the two kernels do not run at the same time: a profiler or a
 // runtime setting that serialises dispatches, or a device busy with other work.  A wait
 // that times out where no second launch follows poisons the state with NaN.
 
-// Wait limit of the second carry launch (1 s): it may start while the prep still runs.
+// Wait limit of the second carry launch (1 s); it runs after the prep, so its flags are
+// normally all set.
 constexpr unsigned kRetryWaitTicks = 100000000u;
 
 // Carry launch modes.
 constexpr int kCarryInOrder = 0;  // after the prep on one stream: waits never block
 constexpr int kCarryBeside = 1;   // beside the prep: a timed-out workgroup aborts
-constexpr int kCarryRetry = 2;    // after the first: only its aborted workgroups run
+constexpr int kCarryRetry = 2;    // after the prep: only the first launch's aborted workgroups run
 
 // Within each aligned 32-block, index 16a + 4g + b is stored at 8g + 4a + b.  A 16x16x32
 // MFMA lane of group g then finds its 8 k-values {16a + 4g + b} in one 16-byte run; that
@@ -972,18 +973,19 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
         return e != hipSuccess ? e : carry(kCarryInOrder, wait_ticks);
     }
     // fork: the prep starts after the caller's earlier work; the carry is queued first so its
-    // workgroups take their CUs before the prep fills the rest.  The second carry launch
-    // follows the first directly on the caller's stream: a workgroup that gave up waits for
-    // the flags itself (with a long limit), so it needs no event wait in front of it.  join:
-    // later work on the caller's stream (and the next call's prep) waits for this prep.
+    // workgroups take their CUs before the prep fills the rest.  join: the caller's stream
+    // waits for the prep, then the second carry launch redoes any workgroup that gave up
+    // (and otherwise exits at once).  The second launch must stay behind the join: under a
+    // scheduler that serialises dispatches it could otherwise run before the prep and wait
+    // for flags that cannot come.
     std::lock_guard<std::mutex> lock(g_side_mu);
     hipError_t e = hipEventRecord(side->fork, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(side->s, side->fork, 0);
     if (e == hipSuccess) e = carry(kCarryBeside, wait_ticks);
     if (e == hipSuccess) e = prep(side->s);
     if (e == hipSuccess) e = hipEventRecord(side->join, side->s);
-    if (e == hipSuccess) e = carry(kCarryRetry, kRetryWaitTicks);
     if (e == hipSuccess) e = hipStreamWaitEvent(stream, side->join, 0);
+    if (e == hipSuccess) e = carry(kCarryRetry, kRetryWaitTicks);
     return e;
 }
 }  // namespace
