@@ -145,6 +145,12 @@ gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
     for (int it = 0; it < kR; ++it)
         s[it] = __builtin_nontemporal_load(Sc + it * kLpc + j);
+    // Wait for the state before issuing the q / k / v loads.  Measured over 16 x 32 heads with
+    // 16 replicas cycled: 11.3 vs 12.2 us per step with the small loads issued under the
+    // state loads (and 9.4 vs 10.4 us on a cache-resident state).
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt left at their maxima
+    __builtin_amdgcn_sched_barrier(0);
     if (tid < 64) {  // wave 0 -- lanes 0-31: k row, 32-63: q row, 4 halfs each
         const half_t* row = (tid < 32 ? k : q) + (bt * Hq + hq) * kD;
         kq_rows[tid >> 5][tid & 31] = *reinterpret_cast<const half4_t*>(row + 4 * (tid & 31));
