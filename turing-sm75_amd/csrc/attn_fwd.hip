@@ -295,7 +295,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = max_xor32(mx);
             // Raise the reference max only when some score would exceed it by 2^8 in the
             // exp2 domain (always on the first unmasked tile: m = -inf).
             if (__builtin_amdgcn_ballot_w64((mx - m) * c2 > 8.f)) {
@@ -340,7 +340,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     }
 
     // ---- epilogue: O = O^T / l (times sigmoid(gate)), 4 consecutive d per store ----
-    l += __shfl_xor(l, 32);
+    l = sum_xor32(l);
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (my_q < S) {
         half_t* orow = O + head + (size_t)my_q * D;

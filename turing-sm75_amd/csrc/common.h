@@ -59,6 +59,28 @@ __device__ __forceinline__ float sum8(float x) {
     return x;
 }
 
+// Values of lanes l and l ^ 32 on every lane, from v_permlane32_swap (a VALU exchange of the
+// two wave halves; __shfl_xor goes through ds_bpermute, an LDS round trip): on return lane l
+// holds the pair as {x[l % 32], x[l % 32 + 32]}.  Inline asm, not the builtin: this compiler
+// folds the builtin's second result into its first (r0 + r1 becomes r0 + r0).  The s_nop
+// gives the wait states the compiler puts between a VALU write and this instruction.
+__device__ __forceinline__ void halves32(float x, float& lo, float& hi) {
+    unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    lo = __builtin_bit_cast(float, a);
+    hi = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    float a, b;
+    halves32(x, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    float a, b;
+    halves32(x, a, b);
+    return a + b;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // The gates of the target model's Gated DeltaNet layer: softplus(x) = log(1 + e^x), with x
