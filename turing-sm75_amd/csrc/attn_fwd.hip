@@ -216,127 +216,230 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
             for (int i = 0; i < C::kDBlocks; ++i) asm volatile("" : "+a"(o[i]));
         }
     };
-    for (int t = 0; t < n_tiles; ++t) {
-        pin_o();
-        const int k0 = t * kKRows;
-        const bool more = t + 1 < n_tiles;
-        const unsigned nbuf = lds0 + ((t + 1) & 1) * buf_bytes;
-        if (k0 >= wave_kv_end) {  // this wave's queries end before the tile: copies only
-            if (more) {
-                copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
-                copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
-            }
-        } else {
-            const half_t* Kt = lds + (t & 1) * 2 * C::kTile;
-            const half_t* Vt = Kt + C::kTile;
-            // ---- S^T = K Q^T for two 32-key blocks, the two accumulator chains interleaved ----
-            // K operand reads: at D = 256 (one wave per SIMD, nothing else on the SIMD to run
-            // while a wave waits on LDS) they run kPreK k-steps ahead of their MFMAs, pinned
-            // there by scheduling barriers, and the first half of the next tile's copies moves
-            // to the top so that the whole QK^T block is one basic block the reads can cross.
-            // Measured on the gated GQA layer: 1.15 vs 1.23 ms causal, +8 % non-causal; at
-            // D <= 128 (two waves per SIMD) the read-ahead measured no change.
-            constexpr int kPreK = D == 256 ? 4 : 1;
-            constexpr bool kCopyTop = kPreK > 1;
-            if (kCopyTop && more)
-                copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
-            float16_t s[2] = {float16_t{}, float16_t{}};
-            const half_t* kr0 = Kt + krow * D;
-            const half_t* kr1 = kr0 + 32 * D;
-
-            half8_t ka[C::kKSteps][2];
-            auto read_k = [&](int kk) {
-                const int cofs = ((2 * kk + hi) ^ ksw) * 8;
-                ka[kk][0] = *reinterpret_cast<const half8_t*>(kr0 + cofs);
-                ka[kk][1] = *reinterpret_cast<const half8_t*>(kr1 + cofs);
-            };
+    if constexpr (D <= 128) {
+        // Two tiles per trip: the buffer parity u is then a constant in each copy of the
+        // body and the LDS addresses of the two buffers differ by an immediate offset instead
+        // of being recomputed every tile (2-3 % at D = 64 and 128).
+        for (int t0 = 0; t0 < n_tiles; t0 += 2) {
 #pragma unroll
-            for (int kk = 0; kk < kPreK; ++kk) read_k(kk);
-            if (kPreK > 1) __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int kk = 0; kk < C::kKSteps; ++kk) {
-                if (kk + kPreK < C::kKSteps) read_k(kk + kPreK);
-                s[0] = mfma32(ka[kk][0], qf[kk], s[0]);
-                s[1] = mfma32(ka[kk][1], qf[kk], s[1]);
-                if (kPreK > 1) __builtin_amdgcn_sched_barrier(0);
-                if (!kCopyTop && kk == C::kKSteps / 2 - 1 && more)
+          for (int u = 0; u < 2; ++u) {
+            const int t = t0 + u;
+            if (t >= n_tiles) break;
+            const int k0 = t * kKRows;
+            const bool more = t + 1 < n_tiles;
+            const unsigned nbuf = lds0 + (unsigned)(u ^ 1) * buf_bytes;
+            if (k0 >= wave_kv_end) {  // this wave's queries end before the tile: copies only
+                if (more) {
                     copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
-            }
-            // V^T operands of the first key step, read now so that their LDS time runs under
-            // the softmax (V does not depend on P); a wave reads transposed V at only ~18 B/clk.
-            // At D = 256 the registers are not there (one wave per SIMD already).
-            constexpr bool kPreV = D <= 128;
-            auto read_v = [&](int ks, int db) {
-                const int r0 = 16 * ks + 4 * hi + vj;      // e = 0 row
-                const int r1 = r0 + 8;                       // e = 1 row
-                const int ch = 4 * db + vchunk;
-                const half4_t lo = lds_read_tr16(Vt + r0 * D + chunk_pos<D>(r0, ch) * 8 + vsub);
-                const half4_t up = lds_read_tr16(Vt + r1 * D + chunk_pos<D>(r1, ch) * 8 + vsub);
-                return half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-            };
-            half8_t v0[kPreV ? C::kDBlocks : 1];
-            if (kPreV) {
+                    copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                }
+            } else {
+                const half_t* Kt = lds + u * 2 * C::kTile;
+                const half_t* Vt = Kt + C::kTile;
+                // ---- S^T = K Q^T for two 32-key blocks, the two accumulator chains interleaved;
+                // the first half of the next tile's copies goes out halfway ----
+                float16_t s[2] = {float16_t{}, float16_t{}};
+                const half_t* kr0 = Kt + krow * D;
+                const half_t* kr1 = kr0 + 32 * D;
+#pragma unroll
+                for (int kk = 0; kk < C::kKSteps; ++kk) {
+                    const int cofs = ((2 * kk + hi) ^ ksw) * 8;
+                    s[0] = mfma32(*reinterpret_cast<const half8_t*>(kr0 + cofs), qf[kk], s[0]);
+                    s[1] = mfma32(*reinterpret_cast<const half8_t*>(kr1 + cofs), qf[kk], s[1]);
+                    if (kk == C::kKSteps / 2 - 1 && more)
+                        copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                }
+                // V^T operands of the first key step, read now so that their LDS time runs under
+                // the softmax (V does not depend on P); a wave reads transposed V at ~18 B/clk.
+                auto read_v = [&](int ks, int db) {
+                    const int r0 = 16 * ks + 4 * hi + vj;  // e = 0 row
+                    const int r1 = r0 + 8;                 // e = 1 row
+                    const int ch = 4 * db + vchunk;
+                    const half4_t lo = lds_read_tr16(Vt + r0 * D + chunk_pos<D>(r0, ch) * 8 + vsub);
+                    const half4_t up = lds_read_tr16(Vt + r1 * D + chunk_pos<D>(r1, ch) * 8 + vsub);
+                    return half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+                };
+                half8_t v0[C::kDBlocks];
 #pragma unroll
                 for (int db = 0; db < C::kDBlocks; ++db) v0[db] = read_v(0, db);
-            }
-            // ---- masks: causal diagonal and keys past S ----
-            if ((kCausal && k0 + kKRows - 1 > qw0) || k0 + kKRows > S) {
+                // ---- masks: causal diagonal and keys past S ----
+                if ((kCausal && k0 + kKRows - 1 > qw0) || k0 + kKRows > S) {
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
+                            if ((kCausal && key > my_q) || key >= S) s[kb][r] = -INFINITY;
+                        }
+                }
+                // ---- online softmax (exp2 domain), as in the loop below ----
+                float mx = -INFINITY;
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                        if ((kCausal && key > my_q) || key >= S) s[kb][r] = -INFINITY;
-                    }
+                    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+                mx = max_xor32(mx);
+                if (__builtin_amdgcn_ballot_w64((mx - m) * c2 > 8.f)) {
+                    const float m_new = fmaxf(m, mx);
+                    const float alpha = m_new == -INFINITY ? 1.f : fast_exp2((m - m_new) * c2);
+                    m = m_new;
+                    l *= alpha;
+#pragma unroll
+                    for (int db = 0; db < C::kDBlocks; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                }
+                const float mc = m == -INFINITY ? 0.f : m * c2;
+                half8_t p[4];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        p[2 * kb + (r >> 3)][r & 7] = (half_t)fast_exp2(fmaf(s[kb][r], c2, -mc));
+                const half2_t one2 = {(half_t)1.f, (half_t)1.f};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int w2 = 0; w2 < 4; ++w2)
+                        l = __builtin_amdgcn_fdot2(half2_t{p[i][2 * w2], p[i][2 * w2 + 1]}, one2, l, false);
+                // ---- O^T += V^T P^T at raised priority, the second copy half among the MFMAs ----
+                __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    if (ks == 1 && more)
+                        copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+#pragma unroll
+                    for (int db = 0; db < C::kDBlocks; ++db)
+                        o[db] = mfma32(ks == 0 ? v0[db] : read_v(ks, db), p[ks], o[db]);
+                }
+                __builtin_amdgcn_s_setprio(0);
             }
-            // ---- online softmax (exp2 domain) ----
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-            mx = max_xor32(mx);
-            // Raise the reference max only when some score would exceed it by 2^8 in the
-            // exp2 domain (always on the first unmasked tile: m = -inf).
-            if (__builtin_amdgcn_ballot_w64((mx - m) * c2 > 8.f)) {
-                const float m_new = fmaxf(m, mx);
-                const float alpha = m_new == -INFINITY ? 1.f : fast_exp2((m - m_new) * c2);
-                m = m_new;
-                l *= alpha;
-#pragma unroll
-                for (int db = 0; db < C::kDBlocks; ++db)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-            }
-            const float mc = m == -INFINITY ? 0.f : m * c2;
-            half8_t p[4];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    p[2 * kb + (r >> 3)][r & 7] = (half_t)fast_exp2(fmaf(s[kb][r], c2, -mc));
-            // row sum of the fp16 P that multiplies V, on v_dot2_f32_f16
-            const half2_t one2 = {(half_t)1.f, (half_t)1.f};
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    l = __builtin_amdgcn_fdot2(half2_t{p[i][2 * u], p[i][2 * u + 1]}, one2, l, false);
-            // ---- O^T += V^T P^T (raised priority: the other wave of the SIMD is then mostly in
-            // its QK^T / softmax part, whose instructions fill the gaps between these MFMAs) ----
-            __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                if (ks == 1 && more)
-                    copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
-#pragma unroll
-                for (int db = 0; db < C::kDBlocks; ++db)
-                    o[db] = mfma32(kPreV && ks == 0 ? v0[kPreV ? db : 0] : read_v(ks, db), p[ks], o[db]);
-            }
-            __builtin_amdgcn_s_setprio(0);
-            pin_o();
+            dma_wait_barrier();
+          }
         }
-        dma_wait_barrier();
+    } else {
+        for (int t = 0; t < n_tiles; ++t) {
+            pin_o();
+            const int k0 = t * kKRows;
+            const bool more = t + 1 < n_tiles;
+            const unsigned nbuf = lds0 + ((t + 1) & 1) * buf_bytes;
+            if (k0 >= wave_kv_end) {  // this wave's queries end before the tile: copies only
+                if (more) {
+                    copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                    copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                }
+            } else {
+                const half_t* Kt = lds + (t & 1) * 2 * C::kTile;
+                const half_t* Vt = Kt + C::kTile;
+                // ---- S^T = K Q^T for two 32-key blocks, the two accumulator chains interleaved ----
+                // K operand reads: at D = 256 (one wave per SIMD, nothing else on the SIMD to run
+                // while a wave waits on LDS) they run kPreK k-steps ahead of their MFMAs, pinned
+                // there by scheduling barriers, and the first half of the next tile's copies moves
+                // to the top so that the whole QK^T block is one basic block the reads can cross.
+                // Measured on the gated GQA layer: 1.15 vs 1.23 ms causal, +8 % non-causal; at
+                // D <= 128 (two waves per SIMD) the read-ahead measured no change.
+                constexpr int kPreK = D == 256 ? 4 : 1;
+                constexpr bool kCopyTop = kPreK > 1;
+                if (kCopyTop && more)
+                    copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                float16_t s[2] = {float16_t{}, float16_t{}};
+                const half_t* kr0 = Kt + krow * D;
+                const half_t* kr1 = kr0 + 32 * D;
+
+                half8_t ka[C::kKSteps][2];
+                auto read_k = [&](int kk) {
+                    const int cofs = ((2 * kk + hi) ^ ksw) * 8;
+                    ka[kk][0] = *reinterpret_cast<const half8_t*>(kr0 + cofs);
+                    ka[kk][1] = *reinterpret_cast<const half8_t*>(kr1 + cofs);
+                };
+    #pragma unroll
+                for (int kk = 0; kk < kPreK; ++kk) read_k(kk);
+                if (kPreK > 1) __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+                for (int kk = 0; kk < C::kKSteps; ++kk) {
+                    if (kk + kPreK < C::kKSteps) read_k(kk + kPreK);
+                    s[0] = mfma32(ka[kk][0], qf[kk], s[0]);
+                    s[1] = mfma32(ka[kk][1], qf[kk], s[1]);
+                    if (kPreK > 1) __builtin_amdgcn_sched_barrier(0);
+                    if (!kCopyTop && kk == C::kKSteps / 2 - 1 && more)
+                        copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                }
+                // V^T operands of the first key step, read now so that their LDS time runs under
+                // the softmax (V does not depend on P); a wave reads transposed V at only ~18 B/clk.
+                // At D = 256 the registers are not there (one wave per SIMD already).
+                constexpr bool kPreV = D <= 128;
+                auto read_v = [&](int ks, int db) {
+                    const int r0 = 16 * ks + 4 * hi + vj;      // e = 0 row
+                    const int r1 = r0 + 8;                       // e = 1 row
+                    const int ch = 4 * db + vchunk;
+                    const half4_t lo = lds_read_tr16(Vt + r0 * D + chunk_pos<D>(r0, ch) * 8 + vsub);
+                    const half4_t up = lds_read_tr16(Vt + r1 * D + chunk_pos<D>(r1, ch) * 8 + vsub);
+                    return half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+                };
+                half8_t v0[kPreV ? C::kDBlocks : 1];
+                if (kPreV) {
+    #pragma unroll
+                    for (int db = 0; db < C::kDBlocks; ++db) v0[db] = read_v(0, db);
+                }
+                // ---- masks: causal diagonal and keys past S ----
+                if ((kCausal && k0 + kKRows - 1 > qw0) || k0 + kKRows > S) {
+    #pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+    #pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
+                            if ((kCausal && key > my_q) || key >= S) s[kb][r] = -INFINITY;
+                        }
+                }
+                // ---- online softmax (exp2 domain) ----
+                float mx = -INFINITY;
+    #pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+    #pragma unroll
+                    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+                mx = max_xor32(mx);
+                // Raise the reference max only when some score would exceed it by 2^8 in the
+                // exp2 domain (always on the first unmasked tile: m = -inf).
+                if (__builtin_amdgcn_ballot_w64((mx - m) * c2 > 8.f)) {
+                    const float m_new = fmaxf(m, mx);
+                    const float alpha = m_new == -INFINITY ? 1.f : fast_exp2((m - m_new) * c2);
+                    m = m_new;
+                    l *= alpha;
+    #pragma unroll
+                    for (int db = 0; db < C::kDBlocks; ++db)
+    #pragma unroll
+                        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                }
+                const float mc = m == -INFINITY ? 0.f : m * c2;
+                half8_t p[4];
+    #pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+    #pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        p[2 * kb + (r >> 3)][r & 7] = (half_t)fast_exp2(fmaf(s[kb][r], c2, -mc));
+                // row sum of the fp16 P that multiplies V, on v_dot2_f32_f16
+                const half2_t one2 = {(half_t)1.f, (half_t)1.f};
+    #pragma unroll
+                for (int i = 0; i < 4; ++i)
+    #pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        l = __builtin_amdgcn_fdot2(half2_t{p[i][2 * u], p[i][2 * u + 1]}, one2, l, false);
+                // ---- O^T += V^T P^T (raised priority: the other wave of the SIMD is then mostly in
+                // its QK^T / softmax part, whose instructions fill the gaps between these MFMAs) ----
+                __builtin_amdgcn_s_setprio(1);
+    #pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    if (ks == 1 && more)
+                        copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+    #pragma unroll
+                    for (int db = 0; db < C::kDBlocks; ++db)
+                        o[db] = mfma32(kPreV && ks == 0 ? v0[kPreV ? db : 0] : read_v(ks, db), p[ks], o[db]);
+                }
+                __builtin_amdgcn_s_setprio(0);
+                pin_o();
+            }
+            dma_wait_barrier();
+        }
     }
 
     // ---- epilogue: O = O^T / l (times sigmoid(gate)), 4 consecutive d per store ----
