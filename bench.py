@@ -13,8 +13,9 @@ One bench step is one pass over the hot path with every input already resident i
     N(0, 0.02)), one per state replica (16 replicas, 512 MiB > the 256 MiB Infinity
     Cache) so every step streams its state from HBM.
 The decode part's figure is the decode workload itself, timed after the step: 512 decode
-steps back to back, cycling the 16 replicas, between one pair of events (a serving loop's
-step time, not one launch's latency); the 16 in-step launches are reported beside it.
+steps back to back, each with its own pre-generated token (fresh q, k, v, g, beta per step),
+cycling the 16 replicas, between one pair of events (a serving loop's step time, not one
+launch's latency); the 16 in-step launches are reported beside it.
 W untimed warmup steps, then exactly K timed steps between two synchronisations.  Each
 kernel's average duration comes from HIP events recorded on the stream it runs on.
 After the timed steps, outside the step, the gated grouped-query attention layer of the
@@ -22,13 +23,15 @@ reference's target model (B=1, 24 query / 4 K/V heads, D=256, S=8192, causal, ga
 softmax) is timed on its own and reported as the part `attn_gqa_gated`; so is the GDN
 recurrence with the layer's pre/post ops at the prefill shape (`gdn_layer_ops`): raw q/k
 and gate projections -> fused chunked prefill -> gated RMSNorm, against the unfused
-pipeline (pre-op pass, chunked prefill, gated RMSNorm).
+pipeline (pre-op pass, chunked prefill, gated RMSNorm); and, for context only, the GDN
+layer at the reference's own published shape (T=512, 16 QK / 48 V heads, its LCG inputs:
+token-serial and chunked, `gdn_reference_shape`) beside its 2080 Ti times.
 
 Printed: one JSON line.  `value` is the attention forward throughput (TFLOP/s, causal
 executed FLOPs 2*B*H*S*(S+1)*D, the convention of src/attn_sm75.cu:534), the kernel that
 dominates the step; `parts` carries all three components, each with its absolute
 throughput, its roofline fraction and a CPU baseline (the oracle, timed on a bounded
-sample on this machine's host cores).
+sample on this machine's host cores, all threads and one thread).
 """
 from __future__ import annotations
 
@@ -51,7 +54,10 @@ ATTN = dict(B=1, H=32, S=8192, D=128, causal=True)
 # the target model's gated attention layer (24 query / 4 K/V heads, head_dim 256)
 GQA = dict(B=1, Hq=24, Hkv=4, S=8192, D=256, causal=True)
 PREFILL = dict(B=1, T=4096, Hq=16, Hv=32, d=128, chunk=64)
-DECODE = dict(B=16, Hq=16, Hv=32, d=128, replicas=16)
+DECODE = dict(B=16, Hq=16, Hv=32, d=128, replicas=16, steps=512)
+# the reference's published GDN shape (docs/kernels.md:31-39): T=512, 16 QK / 48 V heads
+REF_GDN = dict(B=1, T=512, Hq=16, Hv=48, d=128)
+REF_GDN_MS = {"token_serial_occ8": 0.91, "chunked_wmma_cs16": 5.00}  # RTX 2080 Ti, fp32 I/O
 
 
 def attn_flops(B, H, S, D, causal, **_):
@@ -124,16 +130,17 @@ def make_inputs(torch, dev, seed=2026):
     pre["out"] = torch.empty_like(pre["v"])
 
     d = DECODE
+    n = d["steps"]  # every decode step has its own token: [steps][B][...]
     dec = dict(
-        q=l2n(torch.randn(d["B"], d["Hq"], d["d"], device=dev, generator=gen)).half(),
-        k=l2n(torch.randn(d["B"], d["Hq"], d["d"], device=dev, generator=gen)).half(),
-        v=torch.randn(d["B"], d["Hv"], d["d"], device=dev, generator=gen).half(),
-        beta=torch.sigmoid(torch.randn(d["B"], d["Hv"], device=dev, generator=gen)),
-        g=-torch.nn.functional.softplus(torch.randn(d["B"], d["Hv"], device=dev, generator=gen)),
+        q=l2n(torch.randn(n, d["B"], d["Hq"], d["d"], device=dev, generator=gen)).half(),
+        k=l2n(torch.randn(n, d["B"], d["Hq"], d["d"], device=dev, generator=gen)).half(),
+        v=torch.randn(n, d["B"], d["Hv"], d["d"], device=dev, generator=gen).half(),
+        beta=torch.sigmoid(torch.randn(n, d["B"], d["Hv"], device=dev, generator=gen)),
+        g=-torch.nn.functional.softplus(torch.randn(n, d["B"], d["Hv"], device=dev, generator=gen)),
     )
     dec["states"] = [0.02 * torch.randn(d["B"], d["Hv"], d["d"], d["d"], device=dev, generator=gen)
                      for _ in range(d["replicas"])]
-    dec["out"] = torch.empty_like(dec["v"])
+    dec["out"] = torch.empty_like(dec["v"][0])
 
     g = GQA
     gq = dict(
@@ -164,22 +171,55 @@ def layer_inputs(torch, dev, pre):
     return lay
 
 
+def host_info():
+    """The host the CPU baseline ran on: its CPU model, the logical CPUs it has, and the CPUs
+    this process may run on (the box's share)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"cpu_model": model, "nproc": os.cpu_count() or 1, "usable_cpus": usable}
+
+
 def cpu_baselines(torch, a, pre, dec, threads, lay=None):
-    """Time the oracle (the reference's naive paths restated in C++) on bounded samples."""
+    """Time the oracle (the reference's naive paths restated in C++) on bounded samples, with
+    all `threads` OpenMP threads over independent (sequence, head) pairs and with one thread
+    (the reference's gdn_cpu is single-threaded, src/gdn_sm75.cu:1078-1106)."""
     import numpy as np
     import oracle
+    info = host_info()
     res = {}
-    # attention: every causal row of all 32 heads, all host threads
+
+    def entry(value, unit, sample, one_value, one_sample):
+        return dict(value=value, unit=unit, cores=threads, kind="port", sample=sample,
+                    single_thread={"value": one_value, "cores": 1, "sample": one_sample}, **info)
+
+    def clock(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    # attention: every causal row of all 32 heads (all threads), of one head (one thread)
     s = ATTN
     nh = s["H"]
     q, k, v = (a[n][:, :nh].cpu().numpy() for n in ("q", "k", "v"))
     rows = np.arange(nh * s["S"], dtype=np.int64)
-    t0 = time.perf_counter()
-    oracle.attn_rows(q, k, v, rows, True, nthreads=threads)
-    dt = time.perf_counter() - t0
+    dt = clock(lambda: oracle.attn_rows(q, k, v, rows, True, nthreads=threads))
+    dt1 = clock(lambda: oracle.attn_rows(q[:, :1].copy(), k[:, :1].copy(), v[:, :1].copy(),
+                                         rows[:s["S"]], True, nthreads=1))
     fl = attn_flops(1, nh, s["S"], s["D"], True)
-    res["attn_fwd"] = {"value": fl / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-                       "sample": f"all {s['S']} causal rows of {nh} of {s['H']} heads ({dt:.1f} s)"}
+    res["attn_fwd"] = entry(fl / dt / 1e12, "TFLOP/s",
+                            f"all {s['S']} causal rows of {nh} of {s['H']} heads ({dt:.1f} s)",
+                            fl / nh / dt1 / 1e12, f"all {s['S']} causal rows of 1 head ({dt1:.1f} s)")
     # gated GQA layer: every row of the first query-head group (6 heads sharing K/V head 0)
     c = GQA
     gq = a["gqa"]
@@ -187,53 +227,65 @@ def cpu_baselines(torch, a, pre, dec, threads, lay=None):
     qn, gn = (gq[n][:, :grp].cpu().numpy() for n in ("q", "gate"))
     kn, vn = (gq[n][:, :1].cpu().numpy() for n in ("k", "v"))
     rows = np.arange(grp * c["S"], dtype=np.int64)
-    t0 = time.perf_counter()
-    oracle.attn_gqa_rows(qn, kn, vn, gn, rows, True, nthreads=threads)
-    dt = time.perf_counter() - t0
+    dt = clock(lambda: oracle.attn_gqa_rows(qn, kn, vn, gn, rows, True, nthreads=threads))
+    dt1 = clock(lambda: oracle.attn_gqa_rows(qn, kn, vn, gn, rows[:c["S"]], True, nthreads=1))
     fl = attn_flops(1, grp, c["S"], c["D"], True)
-    res["attn_gqa_gated"] = {"value": fl / dt / 1e12, "unit": "TFLOP/s", "cores": threads,
-                             "kind": "port",
-                             "sample": f"all {c['S']} causal rows of {grp} of {c['Hq']} query heads ({dt:.1f} s)"}
-    # prefill: serial recurrence, all 4096 tokens of all 32 V-heads
+    res["attn_gqa_gated"] = entry(fl / dt / 1e12, "TFLOP/s",
+                                  f"all {c['S']} causal rows of {grp} of {c['Hq']} query heads ({dt:.1f} s)",
+                                  fl / grp / dt1 / 1e12,
+                                  f"all {c['S']} causal rows of 1 query head ({dt1:.1f} s)")
+    # prefill: serial recurrence, all 4096 tokens of all 32 V-heads; one thread: 2 V-heads
     p = PREFILL
-    hv_s = 32
     g = lambda n: pre[n].float().cpu().numpy()
-    qn, kn = g("q"), g("k")
-    vn, bn, gn = g("v")[:, :, :hv_s], g("beta")[:, :, :hv_s], g("g")[:, :, :hv_s]
-    st = np.zeros((1, hv_s, p["d"], p["d"]), np.float32)
+    qn, kn, vn, bn, gn = g("q"), g("k"), g("v"), g("beta"), g("g")
+    st = np.zeros((1, p["Hv"], p["d"], p["d"]), np.float32)
     reps = 10
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        oracle.gdn_serial(qn, kn, vn, gn, bn, st, nthreads=threads)
-    dt = time.perf_counter() - t0
-    tok_s = reps * p["B"] * p["T"] / (dt * p["Hv"] / hv_s)
-    res["gdn_prefill"] = {"value": tok_s, "unit": "tok/s", "cores": threads, "kind": "port",
-                          "sample": f"{reps} x T={p['T']} for {hv_s} of {p['Hv']} V-heads ({dt:.1f} s)"}
+    dt = clock(lambda: [oracle.gdn_serial(qn, kn, vn, gn, bn, st, nthreads=threads) for _ in range(reps)])
+    h1 = 2
+    dt1 = clock(lambda: oracle.gdn_serial(qn, kn, vn[:, :, :h1].copy(), gn[:, :, :h1].copy(),
+                                          bn[:, :, :h1].copy(), st[:, :h1].copy(), nthreads=1))
+    res["gdn_prefill"] = entry(reps * p["B"] * p["T"] / dt, "tok/s",
+                               f"{reps} x T={p['T']} for all {p['Hv']} V-heads ({dt:.1f} s)",
+                               p["B"] * p["T"] / (dt1 * p["Hv"] / h1),
+                               f"T={p['T']} for {h1} of {p['Hv']} V-heads, scaled to all ({dt1:.1f} s)")
     # GDN layer ops: the pre-ops, the serial recurrence and the gated RMSNorm on all heads
     if lay is not None:
         ln = lambda n: lay[n].float().cpu().numpy()
-        t0 = time.perf_counter()
-        qn, kn, gg, bb = oracle.gdn_preprocess(ln("q"), ln("k"), ln("a"), ln("b"), ln("dt"), ln("A"))
-        o, _ = oracle.gdn_serial(qn, kn, pre["v"].float().cpu().numpy(), gg, bb,
-                                 np.zeros((1, p["Hv"], p["d"], p["d"]), np.float32), nthreads=threads)
-        oracle.gated_rmsnorm(o, ln("z"), ln("w"))
-        dt = time.perf_counter() - t0
-        res["gdn_layer_ops"] = {"value": p["B"] * p["T"] / dt, "unit": "tok/s", "cores": threads,
-                                "kind": "port",
-                                "sample": f"T={p['T']} x {p['Hv']} V-heads, pre-ops + serial recurrence "
-                                          f"+ gated RMSNorm ({dt:.1f} s)"}
-    # decode: 1024 single-token steps over the full 16 x 32-head state
+
+        def layer(nt, hv):
+            qn, kn, gg, bb = oracle.gdn_preprocess(ln("q"), ln("k"), ln("a")[:, :, :hv],
+                                                   ln("b")[:, :, :hv], ln("dt")[:hv], ln("A")[:hv])
+            o, _ = oracle.gdn_serial(qn, kn, np.ascontiguousarray(vn[:, :, :hv]), gg, bb,
+                                     np.zeros((1, hv, p["d"], p["d"]), np.float32), nthreads=nt)
+            oracle.gated_rmsnorm(o, ln("z")[:, :, :hv], ln("w"))
+
+        dt = clock(lambda: layer(threads, p["Hv"]))
+        dt1 = clock(lambda: layer(1, h1))
+        res["gdn_layer_ops"] = entry(p["B"] * p["T"] / dt, "tok/s",
+                                     f"T={p['T']} x {p['Hv']} V-heads, pre-ops + serial recurrence "
+                                     f"+ gated RMSNorm ({dt:.1f} s)",
+                                     p["B"] * p["T"] / (dt1 * p["Hv"] / h1),
+                                     f"the same for {h1} of {p['Hv']} V-heads, scaled to all ({dt1:.1f} s)")
+    # decode: 1024 single-token steps over the full 16 x 32-head state, each step its own
+    # token (the pre-generated inputs, cycled); one thread: 64 steps
     d = DECODE
-    steps = 1024
-    qd, kd, vd = (dec[n].float().cpu().numpy()[:, None] for n in ("q", "k", "v"))
-    bd, gd = (dec[n].cpu().numpy()[:, None] for n in ("beta", "g"))
-    st = dec["states"][0].cpu().numpy()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        _, st = oracle.gdn_serial(qd, kd, vd, gd, bd, st, nthreads=threads)
-    dt = time.perf_counter() - t0
-    res["gdn_decode"] = {"value": decode_bytes(**d) * steps / dt / 1e9, "unit": "GB/s", "cores": threads,
-                         "kind": "port", "sample": f"{steps} steps of 16 sequences x 32 heads ({dt:.1f} s)"}
+    qd, kd, vd = (dec[n].float().cpu().numpy()[:, :, None] for n in ("q", "k", "v"))
+    bd, gd = (dec[n].cpu().numpy()[:, :, None] for n in ("beta", "g"))
+    st0 = dec["states"][0].cpu().numpy()
+
+    def run_steps(n, nt):
+        st = st0
+        for i in range(n):
+            j = i % d["steps"]
+            _, st = oracle.gdn_serial(qd[j], kd[j], vd[j], gd[j], bd[j], st, nthreads=nt)
+
+    steps, steps1 = 1024, 64
+    dt = clock(lambda: run_steps(steps, threads))
+    dt1 = clock(lambda: run_steps(steps1, 1))
+    res["gdn_decode"] = entry(decode_bytes(**d) * steps / dt / 1e9, "GB/s",
+                              f"{steps} steps of 16 sequences x 32 heads ({dt:.1f} s)",
+                              decode_bytes(**d) * steps1 / dt1 / 1e9,
+                              f"{steps1} steps of 16 sequences x 32 heads ({dt1:.1f} s)")
     return res
 
 
@@ -275,10 +327,17 @@ def main():
         tsa.gdn_chunked_fwd(pre["q"], pre["k"], pre["v"], pre["g"], pre["beta"], pre["state"],
                             pre["out"], ws=ws, stream=stream)
 
+    dstep = [0]  # decode steps issued so far: step i uses token i % 512 of the inputs
+
+    def decode_step(st):
+        j = dstep[0] % DECODE["steps"]
+        dstep[0] += 1
+        tsa.gdn_decode_step(dec["q"][j], dec["k"][j], dec["v"][j], dec["g"][j], dec["beta"][j], st,
+                            dec["out"], stream=stream)
+
     def decode():
         for st in dec["states"]:
-            tsa.gdn_decode_step(dec["q"], dec["k"], dec["v"], dec["g"], dec["beta"], st,
-                                dec["out"], stream=stream)
+            decode_step(st)
 
     parts = [("attn_fwd", attn), ("gdn_prefill", prefill), ("gdn_decode", decode)]
     for _ in range(args.warmup):
@@ -314,19 +373,22 @@ def main():
     ms["gdn_decode"] /= DECODE["replicas"]  # per decode step (one launch)
     ms_step = wall * 1e3 / K
 
-    # decode-only runs: the 512-step workload cycling replicas, and one resident buffer
+    redo = tsa.gdn_chunked_redo_count(ws, PREFILL["B"], PREFILL["T"], PREFILL["Hq"], PREFILL["Hv"],
+                                      stream=stream)
+
+    # decode-only runs: the 512-step workload (each step its own token) cycling replicas,
+    # and one resident buffer
     n = args.decode_steps
+    dstep[0] = 0
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for i in range(n):
-        tsa.gdn_decode_step(dec["q"], dec["k"], dec["v"], dec["g"], dec["beta"],
-                            dec["states"][i % DECODE["replicas"]], dec["out"], stream=stream)
+        decode_step(dec["states"][i % DECODE["replicas"]])
     e1.record(stream)
     e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e2.record(stream)
     for i in range(n):
-        tsa.gdn_decode_step(dec["q"], dec["k"], dec["v"], dec["g"], dec["beta"],
-                            dec["states"][0], dec["out"], stream=stream)
+        decode_step(dec["states"][0])
     e3.record(stream)
     torch.cuda.synchronize()
     dec_rot_ms = e0.elapsed_time(e1) / n
@@ -382,6 +444,37 @@ def main():
     unfused_ms = time_fn(unfused_layer, n_lay)
     rms_ms = time_fn(rms_only, n_lay)
 
+    # context: one GDN layer at the reference's published shape (T=512, Hq=16, Hv=48), with
+    # inputs in the ranges of its LCG generator (src/gdn_sm75.cu:1270-1279), state from zero
+    r = REF_GDN
+    rgen = torch.Generator(device=dev)
+    rgen.manual_seed(11)
+    uni = lambda lo, hi, *shape: lo + (hi - lo) * torch.rand(*shape, device=dev, generator=rgen)
+    rq = uni(-0.1, 0.1, r["B"], r["T"], r["Hq"], r["d"]).half()
+    rk = uni(-0.1, 0.1, r["B"], r["T"], r["Hq"], r["d"]).half()
+    rv = uni(-0.1, 0.1, r["B"], r["T"], r["Hv"], r["d"]).half()
+    rg = uni(-0.225, -0.175, r["B"], r["T"], r["Hv"])
+    rb = uni(0.4, 0.8, r["B"], r["T"], r["Hv"])
+    rst = torch.zeros(r["B"], r["Hv"], r["d"], r["d"], device=dev)
+    ro = torch.empty_like(rv)
+    rws = torch.empty(tsa.gdn_chunked_workspace_bytes(r["B"], r["T"], r["Hq"], r["Hv"]),
+                      dtype=torch.uint8, device=dev)
+
+    def ref_serial():
+        rst.zero_()
+        tsa.gdn_recurrent_fwd(rq, rk, rv, rg, rb, rst, ro, stream=stream)
+
+    def ref_chunked():
+        rst.zero_()
+        tsa.gdn_chunked_fwd(rq, rk, rv, rg, rb, rst, ro, ws=rws, stream=stream)
+
+    def ref_zero():
+        rst.zero_()
+
+    zero_ms = time_fn(ref_zero, 20)
+    ref_serial_ms = time_fn(ref_serial, 20) - zero_ms
+    ref_chunked_ms = time_fn(ref_chunked, 20) - zero_ms
+
     if args.copy_calibration_mib > 0:
         n_el = args.copy_calibration_mib * (1 << 20) // 4
         src = torch.ones(n_el, dtype=torch.float32, device=dev)
@@ -424,6 +517,15 @@ def main():
             "bytes_per_launch": bp,
             "roofline": roof("mfma", pre_tflops, PEAK_MFMA_F16_TFLOPS, "TFLOP/s", "gdn_prefill"),
             "hbm_frac": round(bp / (ms["gdn_prefill"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "carry_workgroups_redone_last_call": redo,
+        },
+        "gdn_reference_shape": {
+            "workload": "context only: one GDN layer at the reference's published shape, B=1 "
+                        "T=512 Hq=16 Hv=48 d=128, fp16 q/k/v in the ranges of its LCG inputs, "
+                        "state from zero (its own figures are fp32 I/O on an RTX 2080 Ti)",
+            "ms_token_serial": round(ref_serial_ms, 5), "ms_chunked": round(ref_chunked_ms, 5),
+            "reference_ms_2080ti": REF_GDN_MS,
+            "reference_source": "docs/kernels.md:31-39, docs/tu102.md:265-274",
         },
         "attn_gqa_gated": {
             "workload": "gated GQA attention fwd B=1 Hq=24 Hkv=4 S=8192 D=256 causal fp16, "
@@ -444,8 +546,9 @@ def main():
                              "GB/s", "gdn_gated_rmsnorm"),
         },
         "gdn_decode": {
-            "workload": f"GDN decode, {n} steps back to back, 16 sequences x 32 V-heads, 128x128 "
-                        "fp32 state, 16 state replicas cycled (512 MiB, streamed from HBM)",
+            "workload": f"GDN decode, {n} steps back to back, each with its own token, 16 sequences "
+                        "x 32 V-heads, 128x128 fp32 state, 16 state replicas cycled (512 MiB, "
+                        "streamed from HBM)",
             "value": round(dec_gbs, 1), "unit": "GB/s", "ms": round(dec_rot_ms, 5),
             "bytes_per_launch": bd,
             "tok_s": round(DECODE["B"] / (dec_rot_ms * 1e-3), 1),
@@ -461,9 +564,10 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baselines(torch, a, pre, dec, omp_threads(), lay)
+        rnd = lambda d: {kk: (round(vv, 4) if isinstance(vv, float) else rnd(vv) if isinstance(vv, dict)
+                              else vv) for kk, vv in d.items()}
         for k, v in cpu.items():
-            out_parts[k]["cpu_baseline"] = {kk: (round(vv, 4) if isinstance(vv, float) else vv)
-                                            for kk, vv in v.items()}
+            out_parts[k]["cpu_baseline"] = rnd(v)
 
     line = {
         "metric": "attn fwd TFLOP/s + GDN prefill tok/s + decode GB/s, % of MI355X roofline",

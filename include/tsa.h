@@ -3,10 +3,15 @@
  *
  * Drop-in boundary for the two hot-path labs of cookys/turing-sm75.  Every entry point
  * takes device pointers to contiguous buffers the caller owns, enqueues work on the
- * given HIP stream (NULL = the default stream) and returns at once; nothing is
- * allocated, nothing is synchronised, no process-global state is mutated.  Errors come
- * back as TSA_* codes, never as exit() or exceptions (the reference's CUDA_CHECK exits,
- * src/attn_sm75.cu:40-48).
+ * given HIP stream (NULL = the default stream) and returns at once: no device memory is
+ * allocated and nothing is synchronised (tsa_gdn_chunked_redo_count, a diagnostic, is the
+ * one synchronous call).  The one piece of process-wide state: the chunked prefill
+ * (tsa_gdn_chunked_fwd and its fused form) runs its two kernels side by side on the
+ * caller's stream and on a second stream of the same device, which it creates with two
+ * events on the first such call on that device (under a mutex) and keeps until the process
+ * ends; the environment variable TSA_GDN_OVERLAP=0 keeps both kernels on the caller's stream
+ * and creates nothing.  Errors come back as TSA_* codes, never as exit() or exceptions (the
+ * reference's CUDA_CHECK exits, src/attn_sm75.cu:40-48).
  *
  * dtypes: q/k/v/o/out are IEEE fp16 (passed as void*), g_log, beta and the GDN state are
  * fp32.  Layouts follow the reference:
@@ -85,13 +90,24 @@ int tsa_attn_gqa_naive(const void* q, const void* k, const void* v, const void* 
  * gdn_chunked_kernel (:192-354) and the two-pass gdn_prep_kernel + gdn_apply_kernel
  * (:896-1073), with the exact intra-chunk inverse (I + A)^-1 (the reference's solve loop,
  * :271-292, is only first-order accurate).  dk = dv = 128, chunk = 64.  ws must hold
- * tsa_gdn_chunked_workspace_bytes(...) bytes of device memory. */
+ * tsa_gdn_chunked_workspace_bytes(...) bytes of device memory, the caller's as the
+ * reference driver owns the two-pass scratch (src/gdn_sm75.cu:1341-1346); its contents on
+ * entry do not matter (each call clears its own ready flags first), and calls that share
+ * one ws must be ordered on one stream. */
 size_t tsa_gdn_chunked_workspace_bytes(int B, int T, int Hq, int Hv, int dk, int dv,
                                        int chunk);
 int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v, const float* g_log,
                         const float* beta, float* state, void* out, int B, int T, int Hq,
                         int Hv, int dk, int dv, int chunk, float scale, void* ws,
                         size_t ws_bytes, void* stream);
+
+/* Diagnostic, no reference counterpart: after a tsa_gdn_chunked_fwd (or fused) call on ws
+ * with these shapes, *count = the number of its state-carrying workgroups that waited longer
+ * than the limit for the side-by-side kernel (a scheduler that did not run the two kernels
+ * together) and were redone by the call's second launch; 0 when the overlap worked.
+ * Synchronises `stream` (a device-to-host copy of the call's abort words). */
+int tsa_gdn_chunked_redo_count(const void* ws, size_t ws_bytes, int B, int T, int Hq, int Hv,
+                               int dk, int dv, int chunk, int* count, void* stream);
 
 /* Token-serial Gated DeltaNet over T tokens (state held on chip for all T).  Replaces the
  * token-serial kernels gdn_serial_kernel, gdn_smem_kernel, gdn_occ/occ2/occ4/occ4p/occ8

@@ -32,11 +32,13 @@ _SIG = {
 
 
 def load():
+    """Load liboracle.so once; TSA_ORACLE_LIB_PATH names another build (the sanitizer run)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise OSError(f"{LIB_PATH} not found: run `make -C oracle`")
-        lib = ctypes.CDLL(LIB_PATH)
+        path = os.environ.get("TSA_ORACLE_LIB_PATH") or LIB_PATH
+        if not os.path.exists(path):
+            raise OSError(f"{path} not found: run `make -C oracle`")
+        lib = ctypes.CDLL(path)
         for name, args in _SIG.items():
             fn = getattr(lib, name)
             fn.argtypes = args

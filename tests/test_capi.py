@@ -112,6 +112,32 @@ def test_gdn_workspace_bytes_scales_with_chunks():
     assert tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32, chunk=32) == 0
 
 
+def test_gdn_redo_count_argument_errors():
+    lib = tsa.load()
+    c = ctypes.c_int(-1)
+    need = tsa.gdn_chunked_workspace_bytes(1, 100, 2, 4)
+    f = lambda ws=DUMMY, nb=need, T=100, dk=128, cnt=ctypes.byref(c): lib.tsa_gdn_chunked_redo_count(
+        ws, nb, 1, T, 2, 4, dk, 128, 64, cnt, NULL)
+    assert f(ws=NULL) == tsa.TSA_ERR_NULL
+    assert f(cnt=None) == tsa.TSA_ERR_NULL
+    assert f(T=0) == tsa.TSA_ERR_SHAPE
+    assert f(dk=64) == tsa.TSA_ERR_UNSUPPORTED
+    assert f(nb=need - 4) == tsa.TSA_ERR_WORKSPACE
+    assert c.value == -1  # nothing was written
+
+
+def test_binding_rejects_wrong_out_shape(monkeypatch):
+    # the binding's output check runs before any library call: a smaller out would be written
+    # past its end (CPU tensors stand in here, so the device check is bypassed)
+    import torch
+    monkeypatch.setattr(tsa, "_need", lambda *a, **k: None)
+    like = torch.empty(1, 70, 2, 128, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        tsa._out(torch.empty(1, 69, 2, 128, dtype=torch.float16), like)
+    ok = torch.empty_like(like)
+    assert tsa._out(ok, like) is ok
+
+
 def test_gdn_recurrent_and_decode_argument_errors():
     lib = tsa.load()
     args = [DUMMY] * 7

@@ -199,6 +199,78 @@ def test_chunked_carry_gives_up_and_is_redone(dev, orc, monkeypatch):
     _check(o1, s1, o_ref, s_ref, *TOL["chunked"], label="chunked, carry waits limited to 0")
 
 
+def _ws_fill(ws, kind):
+    import torch
+    if kind == "ones":      # every flag and abort word reads 1 ("ready", "redo")
+        ws.view(torch.int32)[:] = 1
+    elif kind == "ff":
+        ws.fill_(255)
+    else:
+        g = torch.Generator(device=ws.device)
+        g.manual_seed(9)
+        ws.copy_(torch.randint(0, 256, ws.shape, generator=g, device=ws.device, dtype=torch.uint8))
+
+
+@pytest.mark.parametrize("wait_us", [None, "0"])
+def test_chunked_workspace_contents_do_not_matter(dev, monkeypatch, wait_us):
+    """Each call clears its own ready flags and abort words before its kernels read them, so a
+    workspace holding any bytes -- in particular flags that already read as published --
+    gives results bit-identical to a zeroed one, with the overlap working normally and with
+    every carry wait cut to zero."""
+    import torch
+    if wait_us is not None:
+        monkeypatch.setenv("TSA_GDN_CARRY_WAIT_US", wait_us)
+    rng = np.random.default_rng(406)
+    B, T, Hq, Hv = 1, 1024, 16, 32
+    q, k, v, g, beta, st = _inputs(rng, B, T, Hq, Hv, sstd=0.02)
+    tq, tk, tv, tg, tb = _dev(dev, q, k, v, g, beta)
+    need = tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv)
+    assert need % 4 == 0
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    ts = _dev(dev, st)[0]
+    o0 = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, ws=ws).clone()
+    s0 = ts.clone()
+    for kind in ("ones", "ff", "random"):
+        _ws_fill(ws, kind)
+        ts.copy_(_dev(dev, st)[0])
+        o1 = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, ws=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o0) and torch.equal(ts, s0), kind
+        n = tsa.gdn_chunked_redo_count(ws, B, T, Hq, Hv)
+        print(f"workspace {kind}: redone carry workgroups {n}")
+        assert 0 <= n <= B * Hv * 4
+
+
+def test_chunked_in_order_opt_out(dev, monkeypatch):
+    """TSA_GDN_OVERLAP=0 runs the prep and the carry in order on the caller's stream: the same
+    results bit for bit, and no carry workgroup is ever redone."""
+    import torch
+    rng = np.random.default_rng(407)
+    B, T, Hq, Hv = 2, 500, 4, 8
+    q, k, v, g, beta, st = _inputs(rng, B, T, Hq, Hv, sstd=0.02)
+    o0, s0 = _gpu(dev, "chunked", q, k, v, g, beta, st)
+    monkeypatch.setenv("TSA_GDN_OVERLAP", "0")
+    tq, tk, tv, tg, tb, ts = _dev(dev, q, k, v, g, beta, st)
+    ws = torch.empty(tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv), dtype=torch.uint8, device=dev)
+    _ws_fill(ws, "ones")
+    o1 = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, ws=ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(o1.float().cpu().numpy(), o0) and np.array_equal(ts.cpu().numpy(), s0)
+    assert tsa.gdn_chunked_redo_count(ws, B, T, Hq, Hv) == 0
+
+
+def test_wrong_out_shape_raises_before_launch(dev):
+    import torch
+    rng = np.random.default_rng(408)
+    q, k, v, g, beta, st = _dev(dev, *_inputs(rng, 1, 70, 1, 2))
+    bad = torch.empty(1, 69, 2, D, dtype=torch.float16, device=dev)
+    for fn in (tsa.gdn_chunked_fwd, tsa.gdn_recurrent_fwd):
+        with pytest.raises(ValueError):
+            fn(q, k, v, g, beta, st, out=bad)
+    with pytest.raises(ValueError):
+        tsa.gdn_decode_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], beta[:, 0], st, out=bad[:, 0, :1])
+
+
 _SERIAL_CHILD = r"""
 import sys
 import numpy as np

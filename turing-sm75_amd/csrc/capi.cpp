@@ -134,6 +134,18 @@ extern "C" int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v,
                                      as_stream(stream)));
 }
 
+extern "C" int tsa_gdn_chunked_redo_count(const void* ws, size_t ws_bytes, int B, int T, int Hq,
+                                          int Hv, int dk, int dv, int chunk, int* count,
+                                          void* stream) {
+    if (!ws || !count) return TSA_ERR_NULL;
+    if (B < 1 || T < 1 || Hq < 1 || Hv < 1 || chunk < 1) return TSA_ERR_SHAPE;
+    if (dk != 128 || dv != 128 || chunk != 64) return TSA_ERR_UNSUPPORTED;
+    const long long nch = (T + 63LL) / 64;
+    if (!fits_int(B, Hv, nch) || !fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
+    if (ws_bytes < tsa::gdn_chunked_ws_bytes(B, T, Hv)) return TSA_ERR_WORKSPACE;
+    return from_hip(tsa::gdn_chunked_redo_count(ws, B, T, Hv, count, as_stream(stream)));
+}
+
 extern "C" int tsa_gdn_recurrent_fwd(const void* q, const void* k, const void* v,
                                      const float* g_log, const float* beta, float* state,
                                      void* out, int B, int T, int Hq, int Hv, int dk, int dv,

@@ -27,10 +27,9 @@
 //   ahead with gfx950 LDS-DMA (global_load_lds_dwordx4) into double-buffered slots, so no
 //   register holds prefetched data and each wave reads its MFMA operands from LDS in
 //   batches ahead of the MFMAs.
-#include <atomic>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
-#include <random>
 #include <type_traits>
 
 #include "common.h"
@@ -54,20 +53,22 @@ constexpr int kWsAqk = kWsU + kC * kD * 2;  // fp16 [64 t][64]: column s stored 
 constexpr int kWsG = kWsAqk + kC * kC * 2;
 constexpr int kWsChunk = kWsG + kC * 16;    // 41984 B, multiple of 256
 
-// Ready flags, after all chunk workspaces: one word per (b, h, chunk).  The prep writes the
-// call's epoch there once the chunk's workspace is in memory; the carry's DMA waves wait
-// for it before copying the chunk.  Epochs differ from call to call, so flags left by an
-// earlier call never read as ready and nothing has to clear them.
+// Ready flags, after all chunk workspaces: one word per (b, h, chunk), then an abort word per
+// carry workgroup.  Every call first clears them with a small kernel on the caller's stream
+// (gdn_flags_clear, a kernel rather than a memset so that a captured graph replays it
+// correctly), so whatever the workspace held before, no flag reads as set before the prep
+// sets it in this call.  The prep writes 1 there once the chunk's workspace is in memory;
+// the carry's DMA waves wait for it before copying the chunk.
 // A wait gives up after a limit on the 100 MHz real-time counter (2 ms; the environment
 // variable TSA_GDN_CARRY_WAIT_US sets it in microseconds, 0 = give up whenever a chunk is
 // not ready at the first look, which is how the tests exercise the path).  When the prep
 // runs beside the carry, a workgroup that gave up leaves its state columns untouched and
-// writes the call's epoch to its abort word (after the ready flags, one per carry
-// workgroup); a second launch of the carry, ordered after the prep on the caller's stream,
-// runs exactly the workgroups whose abort word holds the epoch and exits at once in the
+// writes 1 to its abort word; a second launch of the carry, ordered after the prep on the
+// caller's stream, runs exactly the workgroups whose abort word is 1 and exits at once in the
 // others.  Waits time out when the two kernels do not run at the same time: a profiler or a
-// runtime setting that serialises dispatches, or a device busy with other work.  A wait
-// that times out where no second launch follows poisons the state with NaN.
+// runtime setting that serialises dispatches, or a device busy with other work.  The abort
+// words stay in the workspace after the call (tsa_gdn_chunked_redo_count reads them).  A
+// wait that times out where no second launch follows poisons the state with NaN.
 
 // Wait limit of the second carry launch (1 s); it runs after the prep, so its flags are
 // normally all set.
@@ -171,7 +172,7 @@ __global__ void __launch_bounds__(kThreads, 4)
 gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
                const half_t* __restrict__ v, const float* __restrict__ g_log,
                const float* __restrict__ beta, GdnRawGates gates, unsigned char* __restrict__ ws,
-               unsigned* __restrict__ flags, unsigned epoch, int T, int Hq, int Hv, int nch, int BHv) {
+               unsigned* __restrict__ flags, int T, int Hq, int Hv, int nch, int BHv) {
     __shared__ PrepLds sm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hi = lane >> 5;
     // chunk-major: workgroups are dispatched in the order the carry consumes chunks, and
@@ -427,7 +428,7 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __builtin_amdgcn_s_barrier();
     if (tid == 0)
-        __hip_atomic_store(flags + (size_t)bh * nch + ch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(flags + (size_t)bh * nch + ch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------------------------------------
@@ -530,7 +531,7 @@ __device__ __forceinline__ void dma_wait_barrier() {
 template <int W>
 __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const unsigned char* kh,
                                          const unsigned char* qh, const unsigned char* wsh,
-                                         const unsigned* fl, unsigned epoch, unsigned wait_ticks,
+                                         const unsigned* fl, unsigned wait_ticks,
                                          int* err, unsigned rowbytes, int pair, int T, int nch) {
     constexpr int kJ = (kDmaN - W + 3) / 4;
     const int lane = threadIdx.x & 63;
@@ -577,9 +578,9 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
     auto now = []() { return __builtin_amdgcn_readfirstlane((unsigned)__builtin_amdgcn_s_memrealtime()); };
     auto ready = [&](int n, unsigned v) {
         v = __builtin_amdgcn_readfirstlane(v);
-        if (v == epoch || *err) return;
+        if (v != 0u || *err) return;
         const unsigned t0 = now();
-        while (v != epoch) {
+        while (v == 0u) {
             if (now() - t0 >= wait_ticks) {
                 *err = 1;
                 return;
@@ -774,13 +775,13 @@ __device__ __forceinline__ void out_flush(const half_t* ostage, half_t* out, int
 __global__ void __launch_bounds__(kCarryThreads, 1)
 gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
                 const unsigned char* __restrict__ ws, const unsigned* __restrict__ flags,
-                unsigned* __restrict__ aborts, unsigned epoch, int mode, unsigned wait_ticks,
+                unsigned* __restrict__ aborts, int mode, unsigned wait_ticks,
                 float* __restrict__ state,
                 half_t* __restrict__ out, int T, int Hq, int Hv, int nch, int BHv, float scale) {
     __shared__ CarryLds sm;
     if (mode == kCarryRetry &&
         __builtin_amdgcn_readfirstlane(__hip_atomic_load(aborts + blockIdx.x, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT)) != epoch)
+                                                         __HIP_MEMORY_SCOPE_AGENT)) == 0u)
         return;  // this workgroup finished in the launch beside the prep
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: role branches are scalar
@@ -842,20 +843,20 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
         const unsigned* fl = flags + (size_t)bh * nch;
         int* err = &sm.err[wave - 4];
         switch (wave) {
-            case 4: dma_role<0>(slot_lds, kh, qh, wsh, fl, epoch, wait_ticks, err, rowbytes, pair, T, nch); break;
-            case 5: dma_role<1>(slot_lds, kh, qh, wsh, fl, epoch, wait_ticks, err, rowbytes, pair, T, nch); break;
-            case 6: dma_role<2>(slot_lds, kh, qh, wsh, fl, epoch, wait_ticks, err, rowbytes, pair, T, nch); break;
-            default: dma_role<3>(slot_lds, kh, qh, wsh, fl, epoch, wait_ticks, err, rowbytes, pair, T, nch); break;
+            case 4: dma_role<0>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, pair, T, nch); break;
+            case 5: dma_role<1>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, pair, T, nch); break;
+            case 6: dma_role<2>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, pair, T, nch); break;
+            default: dma_role<3>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, pair, T, nch); break;
         }
     }
     if (chain) {
         // a timed-out wait means some chunk operands were read before they were published:
         // beside the prep, leave the state for the second launch; otherwise poison it
         const bool lost = (sm.err[0] | sm.err[1] | sm.err[2] | sm.err[3]) != 0;
-        // the abort word is written by every launch beside the prep (epoch or 0), so a value
-        // left by an earlier call never sends a finished workgroup into the second launch
-        if (mode == kCarryBeside && tid == 0)
-            __hip_atomic_store(aborts + blockIdx.x, lost ? epoch : 0u, __ATOMIC_RELAXED,
+        // the abort word (cleared at the start of the call) sends this workgroup into the
+        // second launch
+        if (mode == kCarryBeside && tid == 0 && lost)
+            __hip_atomic_store(aborts + blockIdx.x, 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         if (!(lost && mode == kCarryBeside)) {
             const float nan = __builtin_nanf("");
@@ -867,6 +868,12 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
     } else if (outw) {
         out_flush(sm.OS[wave - 2], out, b, T, Hv, h, (nch - 1) * kC, pair, wave - 2);
     }
+}
+
+// Clears the ready flags and abort words of a call (n words) before anything reads them.
+__global__ void __launch_bounds__(256) gdn_flags_clear(unsigned* __restrict__ w, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) w[i] = 0u;
 }
 
 }  // namespace
@@ -883,7 +890,8 @@ namespace {
 // The prep runs on a second stream of the device so that it overlaps the carry: the carry
 // copies a chunk's operands as soon as the prep has published them (ready flags), and the
 // chunk-major prep order produces them in the order the carry consumes them.  One side
-// stream and its fork / join events per device, created on first use.
+// stream and its fork / join events per device, created on the first call that overlaps on
+// that device and kept until the process ends (the library's only process-wide state).
 struct SideStream {
     bool tried = false, ok = false;
     int cus = 0;
@@ -894,30 +902,28 @@ constexpr int kMaxDevices = 64;
 std::mutex g_side_mu;
 SideStream g_side[kMaxDevices];
 
-// Per-process epochs, started from a random point so that flags left in memory by another
-// process are unlikely to read as this call's.
-unsigned next_epoch() {
-    static std::atomic<unsigned> counter{std::random_device{}()};
-    unsigned e = ++counter;
-    return e ? e : ++counter;
+// A positive integer from the environment, or `def` when unset or malformed.
+long env_long(const char* name, long def, long hi) {
+    const char* e = std::getenv(name);
+    if (!e || !*e) return def;
+    char* end = nullptr;
+    const long v = std::strtol(e, &end, 10);
+    return (end && *end == 0 && v >= 0 && v <= hi) ? v : def;
 }
 
 // Longest wait of a carry workgroup for a chunk, in ticks of the 100 MHz real-time counter.
-unsigned carry_wait_ticks() {
-    const char* e = std::getenv("TSA_GDN_CARRY_WAIT_US");
-    long us = 2000;
-    if (e && *e) {
-        char* end = nullptr;
-        const long v = std::strtol(e, &end, 10);
-        if (end && *end == 0 && v >= 0 && v <= 10000000) us = v;
-    }
-    return (unsigned)(us * 100);
-}
+unsigned carry_wait_ticks() { return (unsigned)(env_long("TSA_GDN_CARRY_WAIT_US", 2000, 10000000) * 100); }
+
+// TSA_GDN_OVERLAP=0 runs the prep and the carry in order on the caller's stream (no side
+// stream): for schedulers that cannot run the two kernels side by side, where every call
+// would otherwise wait out the carry's time limit before its second launch.
+bool overlap_allowed() { return env_long("TSA_GDN_OVERLAP", 1, 1) != 0; }
 
 template <bool kFused>
 hipError_t launch_chunked(const void* q, const void* k, const void* v, const float* g_log,
                           const float* beta, const GdnRawGates& gates, float* state, void* out,
-                          int B, int T, int Hq, int Hv, float scale, void* ws, hipStream_t stream) {
+                          int B, int T, int Hq, int Hv, float scale, void* ws, bool may_overlap,
+                          hipStream_t stream) {
     const int nch = (T + kC - 1) / kC;
     const int BHv = B * Hv;
     const int carry_wgs = BHv * (kD / (16 * kStrips));
@@ -926,18 +932,22 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
     auto W = static_cast<unsigned char*>(ws);
     unsigned* flags = reinterpret_cast<unsigned*>(W + (size_t)BHv * nch * kWsChunk);
     unsigned* aborts = flags + (size_t)BHv * nch;
-    const unsigned epoch = next_epoch();
+    const int nflags = BHv * nch + carry_wgs;
     const unsigned wait_ticks = carry_wait_ticks();
+    auto clear = [&]() {
+        hipLaunchKernelGGL(gdn_flags_clear, dim3((nflags + 255) / 256), dim3(256), 0, stream, flags, nflags);
+        return hipGetLastError();
+    };
     auto prep = [&](hipStream_t st) {
         hipLaunchKernelGGL(gdn_chunk_prep<kFused>, dim3(BHv * nch), dim3(kThreads), 0, st, Q, K,
-                           static_cast<const half_t*>(v), g_log, beta, gates, W, flags, epoch, T,
-                           Hq, Hv, nch, BHv);
+                           static_cast<const half_t*>(v), g_log, beta, gates, W, flags, T, Hq, Hv,
+                           nch, BHv);
         return hipGetLastError();
     };
     auto carry = [&](int mode, unsigned ticks) {
         hipLaunchKernelGGL(gdn_chunk_carry, dim3(carry_wgs), dim3(kCarryThreads), 0, stream, Q, K, W,
-                           flags, aborts, epoch, mode, ticks, state, static_cast<half_t*>(out), T,
-                           Hq, Hv, nch, BHv, scale);
+                           flags, aborts, mode, ticks, state, static_cast<half_t*>(out), T, Hq, Hv,
+                           nch, BHv, scale);
         return hipGetLastError();
     };
 
@@ -949,10 +959,10 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
     // The side stream belongs to the device of the caller's stream (the null stream: the
     // current device), which need not be the current device.
     int dev = -1;
-    const bool have_dev = stream ? hipStreamGetDevice(stream, &dev) == hipSuccess
-                                 : hipGetDevice(&dev) == hipSuccess;
     SideStream* side = nullptr;
-    if (cap == hipStreamCaptureStatusNone && have_dev && dev >= 0 && dev < kMaxDevices) {
+    if (may_overlap && nch > 1 && cap == hipStreamCaptureStatusNone && overlap_allowed() &&
+        (stream ? hipStreamGetDevice(stream, &dev) == hipSuccess : hipGetDevice(&dev) == hipSuccess) &&
+        dev >= 0 && dev < kMaxDevices) {
         std::lock_guard<std::mutex> lock(g_side_mu);
         SideStream& d = g_side[dev];
         if (!d.tried) {  // create the stream and events on that device
@@ -966,20 +976,22 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
                    hipEventCreateWithFlags(&d.join, hipEventDisableTiming) == hipSuccess;
             if (switched) (void)hipSetDevice(cur);
         }
-        if (d.ok && 2 * carry_wgs <= d.cus && nch > 1) side = &d;
+        if (d.ok && 2 * carry_wgs <= d.cus) side = &d;
     }
+    hipError_t e = clear();
+    if (e != hipSuccess) return e;
     if (!side) {
-        hipError_t e = prep(stream);
+        e = prep(stream);
         return e != hipSuccess ? e : carry(kCarryInOrder, wait_ticks);
     }
-    // fork: the prep starts after the caller's earlier work; the carry is queued first so its
-    // workgroups take their CUs before the prep fills the rest.  join: the caller's stream
-    // waits for the prep, then the second carry launch redoes any workgroup that gave up
-    // (and otherwise exits at once).  The second launch must stay behind the join: under a
-    // scheduler that serialises dispatches it could otherwise run before the prep and wait
-    // for flags that cannot come.
+    // fork: the prep starts after the caller's earlier work (the flag clear included); the
+    // carry is queued first so its workgroups take their CUs before the prep fills the rest.
+    // join: the caller's stream waits for the prep, then the second carry launch redoes any
+    // workgroup that gave up (and otherwise exits at once).  The second launch must stay
+    // behind the join: under a scheduler that serialises dispatches it could otherwise run
+    // before the prep and wait for flags that cannot come.
     std::lock_guard<std::mutex> lock(g_side_mu);
-    hipError_t e = hipEventRecord(side->fork, stream);
+    e = hipEventRecord(side->fork, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(side->s, side->fork, 0);
     if (e == hipSuccess) e = carry(kCarryBeside, wait_ticks);
     if (e == hipSuccess) e = prep(side->s);
@@ -990,18 +1002,36 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
 }
 }  // namespace
 
+hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, int* count, hipStream_t stream) {
+    const size_t nch = (size_t)(T + kC - 1) / kC;
+    const size_t n = (size_t)B * Hv * (kD / (16 * kStrips));
+    const unsigned char* aborts = static_cast<const unsigned char*>(ws) +
+                                  (size_t)B * Hv * nch * (kWsChunk + sizeof(unsigned));
+    unsigned* host = static_cast<unsigned*>(std::malloc(n * sizeof(unsigned)));
+    if (!host) return hipErrorOutOfMemory;
+    hipError_t e = hipMemcpyAsync(host, aborts, n * sizeof(unsigned), hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e == hipSuccess) {
+        int c = 0;
+        for (size_t i = 0; i < n; ++i) c += host[i] != 0u;
+        *count = c;
+    }
+    std::free(host);
+    return e;
+}
+
 hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,
                        const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
                        float scale, void* ws, hipStream_t stream) {
     return launch_chunked<false>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq, Hv,
-                                 scale, ws, stream);
+                                 scale, ws, true, stream);
 }
 
 hipError_t gdn_chunked_fused(const void* q, const void* k, const void* v, const GdnRawGates& gates,
                              float* state, void* out, int B, int T, int Hq, int Hv, float scale,
                              void* ws, hipStream_t stream) {
     return launch_chunked<true>(q, k, v, nullptr, nullptr, gates, state, out, B, T, Hq, Hv, scale,
-                                ws, stream);
+                                ws, true, stream);
 }
 
 }  // namespace tsa

@@ -31,6 +31,9 @@ size_t gdn_chunked_ws_bytes(int B, int T, int Hv);
 hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,
                        const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
                        float scale, void* ws, hipStream_t stream);
+// Carry workgroups of the last call on ws that gave up waiting and were redone by the second
+// launch (synchronises `stream`).
+hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, int* count, hipStream_t stream);
 hipError_t gdn_recurrent(const void* q, const void* k, const void* v, const float* g_log,
                          const float* beta, float* state, void* out, int B, int T, int Hq,
                          int Hv, float scale, hipStream_t stream);

@@ -55,6 +55,7 @@ _SIGNATURES = {
     "tsa_attn_gqa_naive": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp]),
     "tsa_gdn_chunked_workspace_bytes": (_sz, [_i] * 7),
     "tsa_gdn_chunked_fwd": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp, _sz, _vp]),
+    "tsa_gdn_chunked_redo_count": (_i, [_vp, _sz] + [_i] * 7 + [ctypes.POINTER(ctypes.c_int), _vp]),
     "tsa_gdn_recurrent_fwd": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
     "tsa_gdn_decode_step": (_i, [_vp] * 7 + [_i] * 5 + [_f, _vp]),
     "tsa_gdn_naive": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
@@ -78,10 +79,13 @@ class TsaError(RuntimeError):
 _lib = None
 
 
-def load(path: str = LIB_PATH) -> ctypes.CDLL:
-    """Load libtsa.so once (raises OSError with a build hint when it is missing)."""
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load libtsa.so once (raises OSError with a build hint when it is missing).  The
+    environment variable TSA_LIB_PATH names another build of the same library (the tests'
+    sanitizer run uses it)."""
     global _lib
     if _lib is None:
+        path = path or os.environ.get("TSA_LIB_PATH") or LIB_PATH
         if not os.path.exists(path):
             raise OSError(f"{path} not found: build it with `make -C turing-sm75_amd` "
                           "(or __graft_entry__.build())")
@@ -127,6 +131,27 @@ def _need(t, dtype, ndim, name):
 
 def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
+
+
+def _out(out, like, name="out"):
+    """The output tensor: a new one shaped like `like`, or the caller's, which must have
+    exactly that shape (a smaller one would be written past its end)."""
+    import torch
+    if out is None:
+        return torch.empty_like(like)
+    _need(out, like.dtype, like.dim(), name)
+    if out.shape != like.shape:
+        raise ValueError(f"{name}: expected shape {tuple(like.shape)}, got {tuple(out.shape)}")
+    return out
+
+
+def _scratch(nbytes, device, stream):
+    """A workspace for one call.  It is allocated on the stream the kernels run on, so the
+    caching allocator does not hand it out again before they have finished with it."""
+    import torch
+    s = torch.cuda.current_stream(device) if stream is None else stream
+    with torch.cuda.stream(s):
+        return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
 
 
 # ---------------------------------------------------------------------------------------
@@ -223,14 +248,12 @@ def gdn_chunked_fwd(q, k, v, g_log, beta, state, out=None, scale=None, chunk=64,
     """Chunked prefill; state [B, Hv, dv, dk] is updated in place; returns out."""
     import torch
     B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, True)
-    if out is None:
-        out = torch.empty_like(v)
-    _need(out, torch.float16, 4, "out")
+    out = _out(out, v)
     if scale is None:
         scale = 1.0 / math.sqrt(dk)
     need = gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk)
     if ws is None:
-        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        ws = _scratch(need, q.device, stream)
     _check(load().tsa_gdn_chunked_fwd(
         _ptr(q), _ptr(k), _ptr(v), _ptr(g_log), _ptr(beta), _ptr(state), _ptr(out),
         B, T, Hq, Hv, dk, dv, chunk, float(scale), _ptr(ws), ws.numel() * ws.element_size(),
@@ -238,14 +261,21 @@ def gdn_chunked_fwd(q, k, v, g_log, beta, state, out=None, scale=None, chunk=64,
     return out
 
 
+def gdn_chunked_redo_count(ws, B, T, Hq, Hv, dk=128, dv=128, chunk=64, stream=None) -> int:
+    """Carry workgroups of the last chunked call on ws that were redone after a timed-out wait
+    (0 when prep and carry ran side by side); synchronises the stream."""
+    c = ctypes.c_int(-1)
+    _check(load().tsa_gdn_chunked_redo_count(_ptr(ws), ws.numel() * ws.element_size(), B, T, Hq,
+                                             Hv, dk, dv, chunk, ctypes.byref(c), _stream(stream)))
+    return c.value
+
+
 def gdn_recurrent_fwd(q, k, v, g_log, beta, state, out=None, scale=None, stream=None,
                       naive=False):
     """Token-serial recurrence over T tokens (or the naive check kernel); state in place."""
     import torch
     B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, True)
-    if out is None:
-        out = torch.empty_like(v)
-    _need(out, torch.float16, 4, "out")
+    out = _out(out, v)
     if scale is None:
         scale = 1.0 / math.sqrt(dk)
     fn = load().tsa_gdn_naive if naive else load().tsa_gdn_recurrent_fwd
@@ -258,9 +288,7 @@ def gdn_decode_step(q, k, v, g_log, beta, state, out=None, scale=None, stream=No
     """One token per sequence: q/k [B, Hq, dk], v [B, Hv, dv]; state in place."""
     import torch
     B, _, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, False)
-    if out is None:
-        out = torch.empty_like(v)
-    _need(out, torch.float16, 3, "out")
+    out = _out(out, v)
     if scale is None:
         scale = 1.0 / math.sqrt(dk)
     _check(load().tsa_gdn_decode_step(
@@ -294,14 +322,12 @@ def gdn_chunked_fused_fwd(q, k, v, a, b, dt_bias, A, state, out=None, scale=None
     import torch
     B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, a, b, state, True)
     _gates(a, b, dt_bias, A, (B, T), Hv)
-    if out is None:
-        out = torch.empty_like(v)
-    _need(out, torch.float16, 4, "out")
+    out = _out(out, v)
     if scale is None:
         scale = 1.0 / math.sqrt(dk)
     need = gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk)
     if ws is None:
-        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        ws = _scratch(need, q.device, stream)
     _check(load().tsa_gdn_chunked_fused_fwd(
         _ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b), _ptr(dt_bias), _ptr(A), _ptr(state),
         _ptr(out), B, T, Hq, Hv, dk, dv, chunk, float(scale), float(eps), _ptr(ws),
@@ -315,9 +341,7 @@ def gdn_decode_fused_step(q, k, v, a, b, dt_bias, A, state, out=None, scale=None
     import torch
     B, _, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, a, b, state, False)
     _gates(a, b, dt_bias, A, (B,), Hv)
-    if out is None:
-        out = torch.empty_like(v)
-    _need(out, torch.float16, 3, "out")
+    out = _out(out, v)
     if scale is None:
         scale = 1.0 / math.sqrt(dk)
     _check(load().tsa_gdn_decode_fused_step(
@@ -353,9 +377,7 @@ def gdn_gated_rmsnorm(x, z, w, out=None, eps=1e-6, stream=None):
     if z.shape != x.shape or w.numel() != x.shape[3]:
         raise ValueError("inconsistent shapes: x %s z %s w %s" % (tuple(x.shape), tuple(z.shape),
                                                                  tuple(w.shape)))
-    if out is None:
-        out = torch.empty_like(x)
-    _need(out, torch.float16, 4, "out")
+    out = _out(out, x)
     B, T, Hv, dv = x.shape
     _check(load().tsa_gdn_gated_rmsnorm(_ptr(x), _ptr(z), _ptr(w), _ptr(out), B, T, Hv, dv,
                                         float(eps), _stream(stream)))
@@ -402,7 +424,7 @@ def ggml_gated_delta_net(q, k, v, g_log, beta, state, out, state_out=None, scale
     views = [ggml_view(x) for x in (q, k, v, g_log, beta, state, out, state_out)]
     need = int(load().tsa_ggml_gdn_workspace_bytes(ctypes.byref(views[0]), ctypes.byref(views[2])))
     if ws is None:
-        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        ws = _scratch(need, q.device, stream)
     _check(load().tsa_ggml_gated_delta_net(*[ctypes.byref(x) for x in views], float(scale),
                                            _ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))
     return out
