@@ -40,7 +40,8 @@ enum {
     TSA_ERR_UNSUPPORTED = 3, /* a valid shape this build has no kernel for (e.g. D)  */
     TSA_ERR_WORKSPACE = 4,   /* workspace NULL or smaller than *_workspace_bytes     */
     TSA_ERR_LAUNCH = 5,      /* the HIP runtime rejected a launch                    */
-    TSA_ERR_ARG = 6          /* a non-shape argument is invalid (scale not finite...) */
+    TSA_ERR_ARG = 6,         /* a non-shape argument is invalid (scale not finite...) */
+    TSA_ERR_SCRATCH = 7      /* the shapes exceed tsa_gdn_chunked_fwd_noalloc's scratch */
 };
 
 /* Message for a TSA_* code (static storage). */
@@ -100,6 +101,20 @@ int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v, const float
                         const float* beta, float* state, void* out, int B, int T, int Hq,
                         int Hv, int dk, int dv, int chunk, float scale, void* ws,
                         size_t ws_bytes, void* stream);
+
+/* tsa_gdn_chunked_fwd without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference, whose driver allocates the two-pass scratch
+ * itself (src/gdn_sm75.cu:1341-1346).  The workspace is a fixed 64 MiB device array inside
+ * the library, one per GPU, held until the process ends; shapes whose
+ * tsa_gdn_chunked_workspace_bytes(...) exceed 64 MiB return TSA_ERR_SCRATCH (e.g. 32 V-heads
+ * up to T = 3136).  Nothing is allocated, no stream or event is created (the two kernels run
+ * in order on `stream`), and the results equal tsa_gdn_chunked_fwd's.  Every call on a GPU
+ * uses that GPU's one array: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be ordered by the caller. */
+int tsa_gdn_chunked_fwd_noalloc(const void* q, const void* k, const void* v, const float* g_log,
+                                const float* beta, float* state, void* out, int B, int T, int Hq,
+                                int Hv, int dk, int dv, int chunk, float scale, void* stream);
 
 /* Diagnostic, no reference counterpart: after a tsa_gdn_chunked_fwd (or fused) call on ws
  * with these shapes, *count = the number of its state-carrying workgroups that waited longer

@@ -31,7 +31,7 @@ def test_exports_every_declared_symbol():
 def test_version_and_strerror():
     lib = tsa.load()
     assert lib.tsa_version().decode().startswith("tsa ")
-    for code in range(7):
+    for code in range(8):
         assert tsa.strerror(code)
     assert "unknown" in tsa.strerror(99)
 
@@ -110,6 +110,24 @@ def test_gdn_workspace_bytes_scales_with_chunks():
     assert tsa.gdn_chunked_workspace_bytes(2, 4096, 16, 32) == 2 * 32 * per_head(64)
     assert tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32, dk=64) == 0
     assert tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32, chunk=32) == 0
+
+
+def test_gdn_noalloc_argument_errors():
+    # validated before any HIP call; shapes whose workspace exceeds the fixed 64 MiB scratch
+    # are refused with their own code (32 V-heads: T = 3136 fits, T = 3137 does not)
+    lib = tsa.load()
+    f = lambda q=DUMMY, B=1, T=64, Hv=32, dk=128, chunk=64, scale=0.1: lib.tsa_gdn_chunked_fwd_noalloc(
+        q, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, B, T, 16, Hv, dk, 128, chunk, scale, NULL)
+    assert f(q=NULL) == tsa.TSA_ERR_NULL
+    assert f(T=0) == tsa.TSA_ERR_SHAPE
+    assert f(dk=64) == tsa.TSA_ERR_UNSUPPORTED
+    assert f(chunk=16) == tsa.TSA_ERR_UNSUPPORTED
+    assert f(scale=float("nan")) == tsa.TSA_ERR_ARG
+    assert tsa.gdn_chunked_workspace_bytes(1, 3136, 16, 32) <= 64 << 20
+    assert tsa.gdn_chunked_workspace_bytes(1, 3137, 16, 32) > 64 << 20
+    assert f(T=3137) == tsa.TSA_ERR_SCRATCH
+    assert f(B=2, T=1600) == tsa.TSA_ERR_SCRATCH
+    assert "64 MiB" in tsa.strerror(tsa.TSA_ERR_SCRATCH)
 
 
 def test_gdn_redo_count_argument_errors():

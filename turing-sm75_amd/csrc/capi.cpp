@@ -65,6 +65,7 @@ extern "C" const char* tsa_strerror(int code) {
         case TSA_ERR_WORKSPACE: return "workspace is NULL or smaller than the required size";
         case TSA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
         case TSA_ERR_ARG: return "invalid argument (causal not 0/1, scale not finite / not > 0, or eps not finite / not > 0)";
+        case TSA_ERR_SCRATCH: return "the shapes need more than the 64 MiB device scratch of tsa_gdn_chunked_fwd_noalloc (use tsa_gdn_chunked_fwd with a workspace)";
         default: return "unknown tsa error code";
     }
 }
@@ -132,6 +133,21 @@ extern "C" int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v,
     if (!ws || ws_bytes < need) return TSA_ERR_WORKSPACE;
     return from_hip(tsa::gdn_chunked(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale, ws,
                                      as_stream(stream)));
+}
+
+extern "C" int tsa_gdn_chunked_fwd_noalloc(const void* q, const void* k, const void* v,
+                                           const float* g_log, const float* beta, float* state,
+                                           void* out, int B, int T, int Hq, int Hv, int dk, int dv,
+                                           int chunk, float scale, void* stream) {
+    int rc = check_gdn(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale);
+    if (rc) return rc;
+    if (chunk < 1) return TSA_ERR_SHAPE;
+    if (dk != 128 || dv != 128 || chunk != 64) return TSA_ERR_UNSUPPORTED;
+    const long long nch = (T + 63LL) / 64;
+    if (!fits_int(B, Hv, nch) || !fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
+    if (tsa::gdn_chunked_ws_bytes(B, T, Hv) > tsa::gdn_chunked_noalloc_max_bytes()) return TSA_ERR_SCRATCH;
+    return from_hip(tsa::gdn_chunked_noalloc(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale,
+                                             as_stream(stream)));
 }
 
 extern "C" int tsa_gdn_chunked_redo_count(const void* ws, size_t ws_bytes, int B, int T, int Hq,

@@ -1002,6 +1002,57 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
 }
 }  // namespace
 
+// ---- the no-allocation variant ----
+// `scratch` stands in for the caller's workspace: a file-scope device array that each GPU the
+// library runs on holds from the module's load until the process ends.  Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in for the symbol):
+// the device address comes from hipGetSymbolAddress, once per device, on the first call on
+// that device, and is kept in g_scratch.  Every call on a GPU shares that GPU's array and
+// leaves its contents behind; the ready flags and abort words that must start at zero are
+// cleared by the call's first kernel (the rest of the workspace is written before it is
+// read).  Calls that overlap on one GPU race on the array.
+constexpr size_t kScratchBytes = 64ull << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];
+
+hipError_t scratch_address(hipStream_t stream, void** out) {
+    int dev = -1;
+    hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {  // with that device current
+        int cur = -1;
+        if ((e = hipGetDevice(&cur)) != hipSuccess) return e;
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return hipSuccess;
+}
+}  // namespace
+
+size_t gdn_chunked_noalloc_max_bytes() { return kScratchBytes; }
+
+hipError_t gdn_chunked_noalloc(const void* q, const void* k, const void* v, const float* g_log,
+                               const float* beta, float* state, void* out, int B, int T, int Hq,
+                               int Hv, float scale, hipStream_t stream) {
+    void* ws = nullptr;
+    const hipError_t e = scratch_address(stream, &ws);
+    if (e != hipSuccess) return e;
+    // in order on the caller's stream: no side stream or event is ever created here
+    return launch_chunked<false>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq, Hv,
+                                 scale, ws, false, stream);
+}
+
 hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, int* count, hipStream_t stream) {
     const size_t nch = (size_t)(T + kC - 1) / kC;
     const size_t n = (size_t)B * Hv * (kD / (16 * kStrips));

@@ -31,6 +31,13 @@ size_t gdn_chunked_ws_bytes(int B, int T, int Hv);
 hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,
                        const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
                        float scale, void* ws, hipStream_t stream);
+// The chunked prefill without a caller workspace: the library's fixed device scratch array
+// (gdn_chunked_noalloc_max_bytes() bytes per GPU) stands in for it; no allocation, no side
+// stream.  The caller checks gdn_chunked_ws_bytes(...) against the maximum.
+size_t gdn_chunked_noalloc_max_bytes();
+hipError_t gdn_chunked_noalloc(const void* q, const void* k, const void* v, const float* g_log,
+                               const float* beta, float* state, void* out, int B, int T, int Hq,
+                               int Hv, float scale, hipStream_t stream);
 // Carry workgroups of the last call on ws that gave up waiting and were redone by the second
 // launch (synchronises `stream`).
 hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, int* count, hipStream_t stream);

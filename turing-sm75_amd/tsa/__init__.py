@@ -31,6 +31,7 @@ TSA_ERR_UNSUPPORTED = 3
 TSA_ERR_WORKSPACE = 4
 TSA_ERR_LAUNCH = 5
 TSA_ERR_ARG = 6
+TSA_ERR_SCRATCH = 7
 
 TSA_TYPE_F32, TSA_TYPE_F16 = 0, 1
 
@@ -55,6 +56,7 @@ _SIGNATURES = {
     "tsa_attn_gqa_naive": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _i, _vp]),
     "tsa_gdn_chunked_workspace_bytes": (_sz, [_i] * 7),
     "tsa_gdn_chunked_fwd": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp, _sz, _vp]),
+    "tsa_gdn_chunked_fwd_noalloc": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp]),
     "tsa_gdn_chunked_redo_count": (_i, [_vp, _sz] + [_i] * 7 + [ctypes.POINTER(ctypes.c_int), _vp]),
     "tsa_gdn_recurrent_fwd": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
     "tsa_gdn_decode_step": (_i, [_vp] * 7 + [_i] * 5 + [_f, _vp]),
