@@ -108,7 +108,7 @@ int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v, const float
  * itself (src/gdn_sm75.cu:1341-1346).  The workspace is a fixed 64 MiB device array inside
  * the library, one per GPU, held until the process ends; shapes whose
  * tsa_gdn_chunked_workspace_bytes(...) exceed 64 MiB return TSA_ERR_SCRATCH (e.g. 32 V-heads
- * up to T = 3136).  Nothing is allocated, no stream or event is created (the two kernels run
+ * up to T = 2240).  Nothing is allocated, no stream or event is created (the two kernels run
  * in order on `stream`), and the results equal tsa_gdn_chunked_fwd's.  Every call on a GPU
  * uses that GPU's one array: calls that overlap on one GPU (other streams, other host
  * threads) race and must be ordered by the caller. */

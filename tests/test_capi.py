@@ -102,9 +102,9 @@ def test_gdn_chunked_argument_errors():
 
 
 def test_gdn_workspace_bytes_scales_with_chunks():
-    # per (sequence, V-head): a 41 984-byte chunk workspace and a 4-byte ready flag per chunk,
+    # per (sequence, V-head): a 58 368-byte chunk workspace and a 4-byte ready flag per chunk,
     # and a 4-byte abort word for each of the 4 carry workgroups (32 state columns each)
-    per_head = lambda nch: nch * (41984 + 4) + 4 * 4
+    per_head = lambda nch: nch * (58368 + 4) + 4 * 4
     assert tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32) == 32 * per_head(1)
     assert tsa.gdn_chunked_workspace_bytes(1, 65, 16, 32) == 32 * per_head(2)
     assert tsa.gdn_chunked_workspace_bytes(2, 4096, 16, 32) == 2 * 32 * per_head(64)
@@ -114,7 +114,7 @@ def test_gdn_workspace_bytes_scales_with_chunks():
 
 def test_gdn_noalloc_argument_errors():
     # validated before any HIP call; shapes whose workspace exceeds the fixed 64 MiB scratch
-    # are refused with their own code (32 V-heads: T = 3136 fits, T = 3137 does not)
+    # are refused with their own code (32 V-heads: T = 2240 fits, T = 2241 does not)
     lib = tsa.load()
     f = lambda q=DUMMY, B=1, T=64, Hv=32, dk=128, chunk=64, scale=0.1: lib.tsa_gdn_chunked_fwd_noalloc(
         q, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, B, T, 16, Hv, dk, 128, chunk, scale, NULL)
@@ -123,10 +123,10 @@ def test_gdn_noalloc_argument_errors():
     assert f(dk=64) == tsa.TSA_ERR_UNSUPPORTED
     assert f(chunk=16) == tsa.TSA_ERR_UNSUPPORTED
     assert f(scale=float("nan")) == tsa.TSA_ERR_ARG
-    assert tsa.gdn_chunked_workspace_bytes(1, 3136, 16, 32) <= 64 << 20
-    assert tsa.gdn_chunked_workspace_bytes(1, 3137, 16, 32) > 64 << 20
-    assert f(T=3137) == tsa.TSA_ERR_SCRATCH
-    assert f(B=2, T=1600) == tsa.TSA_ERR_SCRATCH
+    assert tsa.gdn_chunked_workspace_bytes(1, 2240, 16, 32) <= 64 << 20
+    assert tsa.gdn_chunked_workspace_bytes(1, 2241, 16, 32) > 64 << 20
+    assert f(T=2241) == tsa.TSA_ERR_SCRATCH
+    assert f(B=2, T=1200) == tsa.TSA_ERR_SCRATCH
     assert "64 MiB" in tsa.strerror(tsa.TSA_ERR_SCRATCH)
 
 

@@ -61,7 +61,9 @@ def _check(o, s, o_ref, s_ref, out_tol, state_tol, label=""):
 
 
 # per-kernel expected accuracy: chunked uses fp16 MFMA operands, the others fp32 FMA
-TOL = {"chunked": (2e-3, 8e-4), "recurrent": (2e-3, 1e-5), "naive": (2e-3, 1e-5)}
+# chunked: U kept in fp32 and the state update fed an exact fp16 hi + lo pair keep the state
+# within 3e-4 relative (measured 3e-6 at T=4096 from zero, 1.4e-4 on the LCG inputs)
+TOL = {"chunked": (2e-3, 3e-4), "recurrent": (2e-3, 1e-5), "naive": (2e-3, 1e-5)}
 
 
 @pytest.mark.parametrize("kind", ["chunked", "recurrent", "naive"])
@@ -71,6 +73,21 @@ def test_golden_fixtures(dev, golden, kind, i):
     q, k, v, gl, beta, s0 = (g[f"c{i}_{n}"] for n in ("q", "k", "v", "g", "beta", "state0"))
     o, s = _gpu(dev, kind, q, k, v, gl, beta, s0.astype(np.float32))
     _check(o, s, g[f"c{i}_out"], g[f"c{i}_state1"], *TOL[kind], label=f"{kind} golden{i}")
+
+
+@pytest.mark.parametrize("kind", ["chunked", "recurrent"])
+def test_slow_decay_nonzero_state(dev, orc, kind):
+    """A slowly decaying gate (g ~ -0.02 per token) keeps the entering N(0, 0.02) state alive
+    across chunks, so the state carried between chunks (the W S product and the update)
+    decides the result, not only each chunk's last tokens."""
+    rng = np.random.default_rng(409)
+    q, k, v, g, beta, st = _inputs(rng, 1, 2048, 16, 32, sstd=0.02)
+    g = (-0.02 * (1 + 0.5 * rng.standard_normal(g.shape))).astype(np.float32)
+    o, s = _gpu(dev, kind, q, k, v, g, beta, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    # fp32 sums in another order than the oracle's over 2048 tokens of a long-lived state
+    tol = TOL[kind] if kind == "chunked" else (2e-3, 1e-4)
+    _check(o, s, o_ref, s_ref, *tol, label=f"{kind} slow decay T=2048 N(0,0.02) state")
 
 
 @pytest.mark.parametrize("kind", ["chunked", "recurrent"])
@@ -119,7 +136,7 @@ def test_state_continuity_prefill_prefill_decode(dev, orc):
     od = tsa.gdn_decode_step(tq, tk, tv, tg, tb, ts)
     torch.cuda.synchronize()
     o = np.concatenate(outs + [od.float().cpu().numpy()[:, None]], axis=1)
-    _check(o, ts.cpu().numpy(), o_ref, s_ref, 2e-3, 8e-4, label="continuity")
+    _check(o, ts.cpu().numpy(), o_ref, s_ref, 2e-3, 3e-4, label="continuity")
 
 
 def _decode_run(dev, q, k, v, g, beta, st):
@@ -293,7 +310,7 @@ o_ref, s_ref = oracle.gdn_serial(q, k, v, g, beta, st)
 eo = float(np.abs(o - o_ref).max())
 es = float(np.abs(ts.cpu().numpy() - s_ref).max() / np.abs(s_ref).max())
 print(f"serialised dispatch: out max-abs {eo:.2e} state rel {es:.2e}", flush=True)
-sys.exit(0 if (eo < 2e-3 and es < 8e-4) else 1)
+sys.exit(0 if (eo < 2e-3 and es < 3e-4) else 1)
 """
 
 

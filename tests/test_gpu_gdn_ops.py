@@ -121,7 +121,7 @@ def test_chunked_fused(dev, orc, case):
     o_ref, s_ref = _ref_recurrence(orc, q, k, v, a, b, dt, A, st)
     eo, es = float(np.abs(o.float().cpu().numpy() - o_ref).max()), _rel(ts.cpu().numpy(), s_ref)
     print(f"chunked fused {case}: out max-abs {eo:.2e}  state rel {es:.2e}")
-    assert eo < min(2e-3, OUT_GATE) and es < min(8e-4, STATE_GATE)
+    assert eo < min(2e-3, OUT_GATE) and es < min(3e-4, STATE_GATE)
 
 
 def test_chunked_fused_matches_preprocess_then_chunked(dev):

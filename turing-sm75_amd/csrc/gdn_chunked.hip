@@ -46,12 +46,12 @@ constexpr int kCarryThreads = 512;  // waves 0-1 chain, 2-3 output, 4-7 DMA
 
 // Workspace per (b, h, chunk).
 constexpr int kWsW = 0;                     // fp16 [64 t][128]: column i stored at perm32(i)
-constexpr int kWsU = kWsW + kC * kD * 2;    // fp16 [8 strip][4 mtile][64 lane][4]
-constexpr int kWsAqk = kWsU + kC * kD * 2;  // fp16 [64 t][64]: column s stored at perm32(s)
+constexpr int kWsU = kWsW + kC * kD * 2;    // fp32 [8 strip][4 mtile][64 lane][4]
+constexpr int kWsAqk = kWsU + kC * kD * 4;  // fp16 [64 t][64]: column s stored at perm32(s)
 // fp32 [64] e^{G_t} qn_t, [64] e^{G_63 - G_t} kn_t, [64] {e^{G_63}, 0, ...}, [64] zeros, where
 // qn_t, kn_t are the l2-norm factors of the fused entry point's raw q / k rows (1 otherwise)
 constexpr int kWsG = kWsAqk + kC * kC * 2;
-constexpr int kWsChunk = kWsG + kC * 16;    // 41984 B, multiple of 256
+constexpr int kWsChunk = kWsG + kC * 16;    // 58368 B, multiple of 256
 
 // Ready flags, after all chunk workspaces: one word per (b, h, chunk), then an abort word per
 // carry workgroup.  Every call first clears them with a small kernel on the caller's stream
@@ -143,7 +143,7 @@ __device__ __forceinline__ int tri_off(int row, int col) {
 }
 
 // 37 KB, so four workgroups share a CU.  Region x holds A and Aqk / Tm during the solve,
-// then V for the W / U products, then the U staging; K's region takes the W staging.
+// then V for the U product; K's region takes the W staging.
 struct PrepLds {
     half_t K[kC * kD];          // K rows, swizzled; W staging at the end
     union {
@@ -155,7 +155,6 @@ struct PrepLds {
             };
         } s;
         half_t V[kC * kD];      // V rows, swizzled
-        half_t Ust[kC * kD];    // U staging
     } x;
     float G[kC];
     float bt[kC];
@@ -346,17 +345,18 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
     }
     lds_barrier();
 
-    // ---- 4. W = Tm diag(beta e^G) K and U = Tm diag(beta) V: the Tm rows become fp16 A
-    // operands in registers, then V goes to LDS over A / Tm ----
-    float16_t w_acc[2], u_acc[2];
+    // ---- 4. W = Tm diag(beta e^G) K and U = Tm diag(beta) V.  The Tm rows become fp16 A
+    // operands in registers; W's products run first, while Tm is still in LDS, then U's
+    // operand is taken as an exact pair of fp16 halves (hi + lo, two MFMAs per step) and V
+    // goes to LDS over A / Tm.  U is kept in fp32 (stored so): rounding its operand or its
+    // value to fp16 were each ~3e-4 of relative state error at T = 4096 ----
+    float16_t u_acc[2];
     {
         const int trow = 32 * mt + (lane & 31);
         const int g16 = lane >> 4;
         const int nks = mt == 0 ? 2 : 4;  // Tm[t < 32][s >= 32] = 0
-        half8_t aw[4], au[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            if (ks >= nks) break;
+        // the 8 Tm values of this lane's operand slots at k-step ks, zero above the diagonal
+        auto tm_row = [&](int ks, float (&x)[8]) {
             // block (trow/16, ks) lies above the diagonal for ks > trow/16: Tm is zero there
             // and the masked read below goes to a stored block instead
             const int base = tri_off(trow, 16 * min(ks, trow >> 4) + 8 * hi);
@@ -364,11 +364,54 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
             const float4 t1v = *reinterpret_cast<const float4*>(&sm.x.s.Tm[base ^ 4]);
             const float tv[8] = {t0v.x, t0v.y, t0v.z, t0v.w, t1v.x, t1v.y, t1v.z, t1v.w};
 #pragma unroll
+            for (int qd = 0; qd < 8; ++qd) x[qd] = (16 * ks + 8 * hi + qd <= trow) ? tv[qd] : 0.f;
+        };
+        {
+            float16_t w_acc[2];
+            half8_t aw[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                if (ks >= nks) break;
+                float x[8];
+                tm_row(ks, x);
+#pragma unroll
+                for (int qd = 0; qd < 8; ++qd) aw[ks][qd] = (half_t)(x[qd] * sm.bg[16 * ks + 8 * hi + qd]);
+            }
+#pragma unroll
+            for (int n2 = 0; n2 < 2; ++n2) {
+                const int ntw = 2 * (wave & 1) + n2;
+                w_acc[n2] = float16_t{};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    if (ks >= nks) break;
+                    const int row0 = 16 * ks + 8 * hi;
+                    const int col0 = 32 * ntw + 16 * (g16 & 1);
+                    const half8_t bk = cat8(tile_read_tr(sm.K, row0, col0), tile_read_tr(sm.K, row0 + 4, col0));
+                    w_acc[n2] = mfma32(aw[ks], bk, w_acc[n2]);
+                }
+            }
+            lds_barrier();  // every wave's K reads done: W is staged over K
+#pragma unroll
+            for (int n2 = 0; n2 < 2; ++n2) {
+                const int cp = perm32(32 * (2 * (wave & 1) + n2) + (lane & 31));
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int t = 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    sm.K[t * kD + cp] = (half_t)w_acc[n2][r];
+                }
+            }
+        }
+        half8_t au[4], al[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            if (ks >= nks) break;
+            float x[8];
+            tm_row(ks, x);
+#pragma unroll
             for (int qd = 0; qd < 8; ++qd) {
-                const int s = 16 * ks + 8 * hi + qd;
-                const float x = (s <= trow) ? tv[qd] : 0.f;  // Tm is lower triangular
-                aw[ks][qd] = (half_t)(x * sm.bg[s]);
-                au[ks][qd] = (half_t)(x * sm.bt[s]);
+                const float y = x[qd] * sm.bt[16 * ks + 8 * hi + qd];
+                au[ks][qd] = (half_t)y;
+                al[ks][qd] = (half_t)(y - (float)au[ks][qd]);
             }
         }
         lds_barrier();
@@ -381,47 +424,37 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 #pragma unroll
         for (int n2 = 0; n2 < 2; ++n2) {
             const int ntw = 2 * (wave & 1) + n2;
-            w_acc[n2] = float16_t{};
             u_acc[n2] = float16_t{};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 if (ks >= nks) break;
                 const int row0 = 16 * ks + 8 * hi;
                 const int col0 = 32 * ntw + 16 * (g16 & 1);
-                const half8_t bk = cat8(tile_read_tr(sm.K, row0, col0), tile_read_tr(sm.K, row0 + 4, col0));
                 const half8_t bv = cat8(tile_read_tr(sm.x.V, row0, col0), tile_read_tr(sm.x.V, row0 + 4, col0));
-                w_acc[n2] = mfma32(aw[ks], bk, w_acc[n2]);
                 u_acc[n2] = mfma32(au[ks], bv, u_acc[n2]);
+                u_acc[n2] = mfma32(al[ks], bv, u_acc[n2]);
             }
         }
     }
-    lds_barrier();
 
-    // ---- 5. stage W and U in their workspace layouts, then 16-byte stores ----
+    // ---- 5. U stored from registers in fp32 (registers 4a..4a+3 are tokens t0..t0+3 of one
+    // column: one 16-byte slot of the carry's layout); W from its staging, 16-byte stores ----
 #pragma unroll
     for (int n2 = 0; n2 < 2; ++n2) {
         const int col = 32 * (2 * (wave & 1) + n2) + (lane & 31);
-        const int cp = perm32(col);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
-            sm.K[t * kD + cp] = (half_t)w_acc[n2][r];  // W staging over K
-        }
-        // U: registers 4a..4a+3 are tokens t0..t0+3 of one column, contiguous in the layout
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
             const int t0 = 32 * mt + 8 * a + 4 * hi;
-            *reinterpret_cast<half4_t*>(&sm.x.Ust[(((col >> 4) * 4 + (t0 >> 4)) * 64 + ((t0 >> 2) & 3) * 16 + (col & 15)) << 2]) =
-                half4_t{(half_t)u_acc[n2][4 * a], (half_t)u_acc[n2][4 * a + 1], (half_t)u_acc[n2][4 * a + 2],
-                        (half_t)u_acc[n2][4 * a + 3]};
+            const int slot = ((col >> 4) * 4 + (t0 >> 4)) * 64 + ((t0 >> 2) & 3) * 16 + (col & 15);
+            store_dev(wsc + kWsU + (size_t)slot * 16,
+                      make_uint4(__float_as_uint(u_acc[n2][4 * a]), __float_as_uint(u_acc[n2][4 * a + 1]),
+                                 __float_as_uint(u_acc[n2][4 * a + 2]), __float_as_uint(u_acc[n2][4 * a + 3])));
         }
     }
-    lds_barrier();
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int id = it * kThreads + tid;
         store_dev(wsc + kWsW + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.K + id * 8));
-        store_dev(wsc + kWsU + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.x.Ust + id * 8));
     }
 
     // ---- 6. publish: every wave's device-scope stores complete, then the chunk's flag ----
@@ -437,7 +470,7 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
 struct ChainSlot {                   // operands of the loop-carried part of one chunk
     half_t K[kC * kD];               // K rows, swizzled (read transposed by the update)
     half_t W[kC * kD];               // W rows (perm32 columns), swizzled
-    half_t U[kStrips * 4 * 64 * 4];  // this workgroup's two U strips, accumulator order
+    float U[kStrips * 4 * 64 * 4];   // this workgroup's two U strips (fp32), accumulator order
     float E[kC];                     // e^{G_t} qn_t (the output's factor; unused here)
     float Dg[kC];                    // e^{G_63 - G_t} kn_t
     float Ec[2 * kC];                // e^{G_63} (the chunk's decay), then zeros
@@ -464,15 +497,15 @@ __device__ __forceinline__ int aqk_off(int r, int c) {
 
 typedef __attribute__((address_space(3))) void* lds_void_t;
 
-// Per-chunk copies into LDS: 62 one-KiB LDS-DMA instructions (global_load_lds_dwordx4,
-// lane l copies 16 bytes to M0 + 16*l).  Instruction n < 37 fills the chain slot at byte
-// 1024*n (K tile n < 16, W tile, U strips 32..35, decay block 36); n >= 37 fills the out slot at
-// byte 1024*(n-37) (Q tile, Aqk tile, E/Dg 61).  The structs' members are laid out in that
+// Per-chunk copies into LDS: 66 one-KiB LDS-DMA instructions (global_load_lds_dwordx4,
+// lane l copies 16 bytes to M0 + 16*l).  Instruction n < 41 fills the chain slot at byte
+// 1024*n (K tile n < 16, W tile, fp32 U strips 32..39, decay block 40); n >= 41 fills the out
+// slot at byte 1024*(n-41) (Q tile, Aqk tile, E/Dg 65).  The structs' members are laid out in that
 // order so that the LDS offset is just 1024 * tile index.  The four DMA waves (4-7) take
 // n = w + 4j; each lane's source offset for its instructions is fixed for the whole loop
 // and computed once, so an instruction costs a scalar M0 write and the DMA itself.
-constexpr int kDmaN = 62, kDmaChain = 37, kDmaPerWave = 16;
-constexpr int kDmaEOut = 61;  // a 512-byte copy: lanes 0-31 only
+constexpr int kDmaN = 66, kDmaChain = 41;
+constexpr int kDmaEOut = 65;  // a 512-byte copy: lanes 0-31 only
 
 // Source byte offset of instruction n for this lane, from the instruction's base pointer:
 // the row base of the chunk's first token (K / Q tiles, rows at rowbytes apart, rows
@@ -489,7 +522,7 @@ __device__ __forceinline__ unsigned dma_src_off(int n, int lane, unsigned rowbyt
             const int P = (i - 16) * 64 + lane, row = P >> 4, cch = (P & 15) ^ swz(row);
             return kWsW + (row * kD + cch * 8) * 2;
         }
-        if (i < 36) return kWsU + pair * 4096 + (i - 32) * 1024 + lane * 16;  // own U strips
+        if (i < 40) return kWsU + pair * 8192 + (i - 32) * 1024 + lane * 16;  // own U strips
         return kWsG + lane * 16;                     // the whole 1-KiB decay block
     }
     if (i < 24) {                                    // Aqk rows, 8-chunk swizzle
@@ -644,11 +677,10 @@ __device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
             aW[mt][kk] = *reinterpret_cast<const half8_t*>(cs.W + off.w[kk] + 16 * mt * kD);
-    half4_t u[4];
-    float4 d4[4];
+    float4 u[4], d4[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-        u[mt] = *reinterpret_cast<const half4_t*>(cs.U + ((sl * 4 + mt) * 64 + lane) * 4);
+        u[mt] = *reinterpret_cast<const float4*>(cs.U + ((sl * 4 + mt) * 64 + lane) * 4);
         d4[mt] = *reinterpret_cast<const float4*>(cs.Dg + 16 * mt + 4 * g);
     }
     const float eGC = cs.Ec[0];
@@ -673,28 +705,37 @@ __device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) wsv[mt] = mfma16(aW[mt][kk], Sb[kk], wsv[mt]);
-    // Vnew = U - W S (lane: column c, tokens 16mt + 4g + r); Vs = Vnew e^{G_C - G_t}
-    half8_t Vn[2], Vs[2];
+    // Vnew = U - W S (lane: column c, tokens 16mt + 4g + r); Vs = Vnew e^{G_C - G_t} as an
+    // exact pair of fp16 halves (hi + lo): its rounding to one fp16 operand was ~3e-4 of
+    // relative state error at T = 4096; the second MFMA per step reuses the K^T operand
+    half8_t Vn[2], Vs[2], Vl[2];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
+        const float uu[4] = {u[mt].x, u[mt].y, u[mt].z, u[mt].w};
         const float dg[4] = {d4[mt].x, d4[mt].y, d4[mt].z, d4[mt].w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float vn = (float)u[mt][r] - wsv[mt][r];
+            const float vn = uu[r] - wsv[mt][r];
             Vn[mt >> 1][4 * (mt & 1) + r] = (half_t)vn;
-            Vs[mt >> 1][4 * (mt & 1) + r] = (half_t)(vn * dg[r]);
+            const float vs = vn * dg[r];
+            const half_t vh = (half_t)vs;
+            Vs[mt >> 1][4 * (mt & 1) + r] = vh;
+            Vl[mt >> 1][4 * (mt & 1) + r] = (half_t)(vs - (float)vh);
         }
     }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) xs[kk * 64 + lane] = __builtin_bit_cast(uint4, Sb[kk]);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) xs[(4 + ks) * 64 + lane] = __builtin_bit_cast(uint4, Vn[ks]);
-    // S = e^{G_C} S + K^T Vs
+    // S = e^{G_C} S + K^T (Vs hi + Vs lo)
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         S[m] *= eGC;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) S[m] = mfma16(aK[m][ks], Vs[ks], S[m]);
+        for (int ks = 0; ks < 2; ++ks) {
+            S[m] = mfma16(aK[m][ks], Vs[ks], S[m]);
+            S[m] = mfma16(aK[m][ks], Vl[ks], S[m]);
+        }
     }
 }
 
