@@ -457,20 +457,21 @@ def main():
     unfused_ms = time_fn(unfused_layer, n_lay)
     rms_ms = time_fn(rms_only, n_lay)
 
-    # context: one GDN layer at the reference's published shape (T=512, Hq=16, Hv=48), with
-    # inputs in the ranges of its LCG generator (src/gdn_sm75.cu:1270-1279), state from zero
+    # context: one GDN layer at the reference's published shape (T=512, Hq=16, Hv=48), fp32
+    # q / k / v / out as the reference's kernels take them (src/gdn_sm75.cu:57-64), inputs in
+    # the ranges of its LCG generator (:1270-1279), state from zero
     r = REF_GDN
     rgen = torch.Generator(device=dev)
     rgen.manual_seed(11)
     uni = lambda lo, hi, *shape: lo + (hi - lo) * torch.rand(*shape, device=dev, generator=rgen)
-    rq = uni(-0.1, 0.1, r["B"], r["T"], r["Hq"], r["d"]).half()
-    rk = uni(-0.1, 0.1, r["B"], r["T"], r["Hq"], r["d"]).half()
-    rv = uni(-0.1, 0.1, r["B"], r["T"], r["Hv"], r["d"]).half()
+    rq = uni(-0.1, 0.1, r["B"], r["T"], r["Hq"], r["d"])
+    rk = uni(-0.1, 0.1, r["B"], r["T"], r["Hq"], r["d"])
+    rv = uni(-0.1, 0.1, r["B"], r["T"], r["Hv"], r["d"])
     rg = uni(-0.225, -0.175, r["B"], r["T"], r["Hv"])
     rb = uni(0.4, 0.8, r["B"], r["T"], r["Hv"])
     rst = torch.zeros(r["B"], r["Hv"], r["d"], r["d"], device=dev)
     ro = torch.empty_like(rv)
-    rws = torch.empty(tsa.gdn_chunked_workspace_bytes(r["B"], r["T"], r["Hq"], r["Hv"]),
+    rws = torch.empty(tsa.gdn_chunked_workspace_bytes(r["B"], r["T"], r["Hq"], r["Hv"], f32=True),
                       dtype=torch.uint8, device=dev)
 
     def ref_serial():
@@ -534,8 +535,8 @@ def main():
         },
         "gdn_reference_shape": {
             "workload": "context only: one GDN layer at the reference's published shape, B=1 "
-                        "T=512 Hq=16 Hv=48 d=128, fp16 q/k/v in the ranges of its LCG inputs, "
-                        "state from zero (its own figures are fp32 I/O on an RTX 2080 Ti)",
+                        "T=512 Hq=16 Hv=48 d=128, fp32 q/k/v/out (its own I/O type) in the ranges "
+                        "of its LCG inputs, state from zero; its figures are from an RTX 2080 Ti",
             "ms_token_serial": round(ref_serial_ms, 5), "ms_chunked": round(ref_chunked_ms, 5),
             "reference_ms_2080ti": REF_GDN_MS,
             "reference_source": "docs/kernels.md:31-39, docs/tu102.md:265-274",

@@ -14,7 +14,8 @@
  * reference's CUDA_CHECK exits, src/attn_sm75.cu:40-48).
  *
  * dtypes: q/k/v/o/out are IEEE fp16 (passed as void*), g_log, beta and the GDN state are
- * fp32.  Layouts follow the reference:
+ * fp32; the *_f32 GDN entry points take q/k/v/out in fp32 as well, the reference's own GDN
+ * I/O (src/gdn_sm75.cu:57-64).  Layouts follow the reference:
  *   attention : Q, K, V, O                [B][H][S][D]     (src/attn_sm75.cu:64,120,254)
  *   grouped   : Q, gate, O [B][Hq][S][D]; K, V [B][Hkv][S][D]; query head h reads K/V
  *               head h / (Hq / Hkv)
@@ -102,6 +103,18 @@ int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v, const float
                         int Hv, int dk, int dv, int chunk, float scale, void* ws,
                         size_t ws_bytes, void* stream);
 
+/* The same prefill with fp32 q, k, v, out (the reference's GDN kernels and gdn_cpu take fp32,
+ * src/gdn_sm75.cu:57-64,1078-1106): the inputs are converted to the fp16 MFMA operands in
+ * registers, never narrowed in memory, and the output is stored in fp32.  Its workspace is
+ * larger (the prep leaves fp16 copies of each chunk's K and Q rows there for the state
+ * carry): tsa_gdn_chunked_workspace_bytes_f32(...). */
+size_t tsa_gdn_chunked_workspace_bytes_f32(int B, int T, int Hq, int Hv, int dk, int dv,
+                                           int chunk);
+int tsa_gdn_chunked_fwd_f32(const float* q, const float* k, const float* v, const float* g_log,
+                            const float* beta, float* state, float* out, int B, int T, int Hq,
+                            int Hv, int dk, int dv, int chunk, float scale, void* ws,
+                            size_t ws_bytes, void* stream);
+
 /* tsa_gdn_chunked_fwd without a workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference, whose driver allocates the two-pass scratch
@@ -116,13 +129,14 @@ int tsa_gdn_chunked_fwd_noalloc(const void* q, const void* k, const void* v, con
                                 const float* beta, float* state, void* out, int B, int T, int Hq,
                                 int Hv, int dk, int dv, int chunk, float scale, void* stream);
 
-/* Diagnostic, no reference counterpart: after a tsa_gdn_chunked_fwd (or fused) call on ws
- * with these shapes, *count = the number of its state-carrying workgroups that waited longer
- * than the limit for the side-by-side kernel (a scheduler that did not run the two kernels
- * together) and were redone by the call's second launch; 0 when the overlap worked.
- * Synchronises `stream` (a device-to-host copy of the call's abort words). */
+/* Diagnostic, no reference counterpart: after a tsa_gdn_chunked_fwd (fused, or with io_f32 = 1
+ * tsa_gdn_chunked_fwd_f32) call on ws with these shapes, *count = the number of its
+ * state-carrying workgroups that waited longer than the limit for the side-by-side kernel (a
+ * scheduler that did not run the two kernels together) and were redone by the call's second
+ * launch; 0 when the overlap worked.  Synchronises `stream` (a device-to-host copy of the
+ * call's abort words). */
 int tsa_gdn_chunked_redo_count(const void* ws, size_t ws_bytes, int B, int T, int Hq, int Hv,
-                               int dk, int dv, int chunk, int* count, void* stream);
+                               int dk, int dv, int chunk, int io_f32, int* count, void* stream);
 
 /* Token-serial Gated DeltaNet over T tokens (state held on chip for all T).  Replaces the
  * token-serial kernels gdn_serial_kernel, gdn_smem_kernel, gdn_occ/occ2/occ4/occ4p/occ8
@@ -131,12 +145,21 @@ int tsa_gdn_recurrent_fwd(const void* q, const void* k, const void* v, const flo
                           const float* beta, float* state, void* out, int B, int T, int Hq,
                           int Hv, int dk, int dv, float scale, void* stream);
 
+/* The same with fp32 q, k, v, out (the reference's token-serial kernels' own I/O). */
+int tsa_gdn_recurrent_fwd_f32(const float* q, const float* k, const float* v, const float* g_log,
+                              const float* beta, float* state, float* out, int B, int T, int Hq,
+                              int Hv, int dk, int dv, float scale, void* stream);
+
 /* One decode step: one token for each of B sequences, q/k [B][Hq][dk], v/out [B][Hv][dv],
  * g_log/beta [B][Hv], state [B][Hv][dv][dk] updated in place.  The T = 1 case of the
  * token-serial kernels (src/gdn_sm75.cu:744-784 with one iteration). */
 int tsa_gdn_decode_step(const void* q, const void* k, const void* v, const float* g_log,
                         const float* beta, float* state, void* out, int B, int Hq, int Hv,
                         int dk, int dv, float scale, void* stream);
+/* The same with fp32 q, k, v, out. */
+int tsa_gdn_decode_step_f32(const float* q, const float* k, const float* v, const float* g_log,
+                            const float* beta, float* state, float* out, int B, int Hq, int Hv,
+                            int dk, int dv, float scale, void* stream);
 
 /* ---- The Gated DeltaNet layer's pre / post ops (the target model's layer,
  * docs/qwen38-27b.md:15).  The reference tree has no implementation of them: its inputs
@@ -207,6 +230,10 @@ int tsa_ggml_gated_delta_net(const tsa_tensor* q, const tsa_tensor* k, const tsa
 int tsa_gdn_naive(const void* q, const void* k, const void* v, const float* g_log,
                   const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
                   int dk, int dv, float scale, void* stream);
+/* The same with fp32 q, k, v, out (the gdn driver's check of its fp32 runs). */
+int tsa_gdn_naive_f32(const float* q, const float* k, const float* v, const float* g_log,
+                      const float* beta, float* state, float* out, int B, int T, int Hq, int Hv,
+                      int dk, int dv, float scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -101,6 +101,23 @@ def test_gdn_chunked_argument_errors():
     assert _chunked(ws_bytes=need - 1) == tsa.TSA_ERR_WORKSPACE
 
 
+def test_gdn_f32_entry_points_validate_like_fp16():
+    lib = tsa.load()
+    args = [DUMMY] * 7
+    need32 = tsa.gdn_chunked_workspace_bytes(1, 100, 2, 4, f32=True)
+    assert need32 == tsa.gdn_chunked_workspace_bytes(1, 100, 2, 4) + 2 * 32768 * 4  # + K, Q rows
+    ch = lambda ws=DUMMY, nb=need32, dk=128, T=100: lib.tsa_gdn_chunked_fwd_f32(
+        *args, 1, T, 2, 4, dk, 128, 64, 0.1, ws, nb, NULL)
+    assert ch(ws=NULL) == tsa.TSA_ERR_WORKSPACE
+    assert ch(nb=need32 - 1) == tsa.TSA_ERR_WORKSPACE
+    assert ch(dk=64) == tsa.TSA_ERR_UNSUPPORTED
+    assert ch(T=0) == tsa.TSA_ERR_SHAPE
+    assert lib.tsa_gdn_recurrent_fwd_f32(*args[:6], NULL, 1, 4, 1, 2, 128, 128, 0.1, NULL) == tsa.TSA_ERR_NULL
+    assert lib.tsa_gdn_decode_step_f32(*args, 4, 1, 2, 128, 96, 0.1, NULL) == tsa.TSA_ERR_UNSUPPORTED
+    assert lib.tsa_gdn_naive_f32(*args, 1, 1, 0, 2, 128, 128, 0.1, NULL) == tsa.TSA_ERR_SHAPE
+    assert lib.tsa_gdn_chunked_workspace_bytes_f32(1, 64, 16, 32, 128, 128, 32) == 0
+
+
 def test_gdn_workspace_bytes_scales_with_chunks():
     # per (sequence, V-head): a 58 368-byte chunk workspace and a 4-byte ready flag per chunk,
     # and a 4-byte abort word for each of the 4 carry workgroups (32 state columns each)
@@ -134,9 +151,11 @@ def test_gdn_redo_count_argument_errors():
     lib = tsa.load()
     c = ctypes.c_int(-1)
     need = tsa.gdn_chunked_workspace_bytes(1, 100, 2, 4)
-    f = lambda ws=DUMMY, nb=need, T=100, dk=128, cnt=ctypes.byref(c): lib.tsa_gdn_chunked_redo_count(
-        ws, nb, 1, T, 2, 4, dk, 128, 64, cnt, NULL)
+    f = lambda ws=DUMMY, nb=need, T=100, dk=128, io=0, cnt=ctypes.byref(c): lib.tsa_gdn_chunked_redo_count(
+        ws, nb, 1, T, 2, 4, dk, 128, 64, io, cnt, NULL)
     assert f(ws=NULL) == tsa.TSA_ERR_NULL
+    assert f(io=2) == tsa.TSA_ERR_ARG
+    assert f(io=1) == tsa.TSA_ERR_WORKSPACE  # the fp32-I/O workspace is larger
     assert f(cnt=None) == tsa.TSA_ERR_NULL
     assert f(T=0) == tsa.TSA_ERR_SHAPE
     assert f(dk=64) == tsa.TSA_ERR_UNSUPPORTED
@@ -172,6 +191,7 @@ def test_gdn_recurrent_and_decode_argument_errors():
     ["attn_sm75", "--causal"],
     ["gdn", "0"],
     ["gdn", "64", "--mode", "train"],
+    ["gdn", "64", "--io", "f64"],
 ])
 def test_drivers_usage_errors_exit_2(argv):
     exe = os.path.join(BIN, argv[0])

@@ -54,7 +54,8 @@ def test_attn_driver(args):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("args", [
-    ["512"],                                     # the reference's `make gdn`: LCG, Hv=48
+    ["512"],                                     # the reference's `make gdn`: LCG, Hv=48, fp32 I/O
+    ["512", "--io", "f16"],                      # the same inputs rounded to fp16 I/O
     ["100"],                                     # ragged T (one full and one partial chunk)
     ["4096", "--hv", "32", "--dist", "normal", "--iters", "5"],   # the prefill workload
     ["--mode", "decode", "--steps", "64"],       # 16 sequences, step-major decode layout

@@ -110,6 +110,55 @@ def test_reference_lcg_shape(dev, orc, kind):
     _check(o, s, o_ref, s_ref, *TOL[kind], label=f"{kind} lcg T=512 Hv=48")
 
 
+@pytest.mark.parametrize("kind", ["chunked", "recurrent", "naive"])
+def test_reference_lcg_shape_fp32_io(dev, orc, kind):
+    """The reference's own GDN workload at its own precision: the driver's LCG inputs in fp32
+    (src/gdn_sm75.cu:1270-1279), T = 512, 16 QK / 48 V heads, through the *_f32 entry points,
+    against the oracle on the same fp32 inputs (gdn_cpu, :1078-1106)."""
+    q, k, v, g, b = orc.gdn_lcg_inputs(512, 16, 48)
+    q, k, v, g, b = (x[None] for x in (q, k, v, g, b))
+    st = np.zeros((1, 48, D, D), np.float32)
+    assert q.dtype == np.float32
+    o, s = _gpu(dev, kind, q, k, v, g, b, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, b, st)
+    # chunked: the fp32 inputs become the fp16 MFMA operands (rounded in registers); a numpy
+    # model puts each of K's and V's roundings at ~2.5e-4 of the state here (3.9e-4 measured),
+    # inside the reference's 1e-3 gate; the token-serial and naive kernels are fp32 throughout
+    tol = (2e-3, 8e-4) if kind == "chunked" else TOL[kind]
+    _check(o, s, o_ref, s_ref, *tol, label=f"{kind} fp32 I/O lcg T=512 Hv=48")
+
+
+@pytest.mark.parametrize("kind", ["chunked", "recurrent"])
+def test_fp32_io_equals_fp16_io_on_fp16_values(dev, kind):
+    """On inputs fp16 represents exactly, the fp32-I/O kernels compute what the fp16 ones do:
+    the same state bit for bit, and the same outputs up to the final rounding.  The fp16 path
+    rounds the scaled output once to fp16 (the multiply by the scale and the conversion fuse),
+    the fp32 path rounds it to fp32: rounding that fp32 value to fp16 again may differ from the
+    fp16 path only where it lies exactly halfway between two fp16 values."""
+    rng = np.random.default_rng(410)
+    q, k, v, g, beta, st = _inputs(rng, 2, 300, 4, 8, sstd=0.02)
+    o16, s16 = _gpu(dev, kind, q, k, v, g, beta, st)
+    f = lambda x: x.astype(np.float32)
+    o32, s32 = _gpu(dev, kind, f(q), f(k), f(v), g, beta, st)
+    assert np.array_equal(s32, s16)
+    h = o16.astype(np.float16)
+    r = o32.astype(np.float16)
+    other = np.nextafter(h, np.where(o32 > h, np.float16(np.inf), np.float16(-np.inf)).astype(np.float16))
+    tie = o32.astype(np.float64) == (h.astype(np.float64) + other.astype(np.float64)) / 2
+    print(f"{kind}: {int((r != h).sum())} of {r.size} outputs differ after rounding, all at fp16 ties")
+    assert np.all((r == h) | tie)
+
+
+def test_decode_fp32_io(dev, orc):
+    rng = np.random.default_rng(411)
+    q, k, v, g, beta, st = _inputs(rng, 4, 6, 2, 4, sstd=0.02)
+    f = lambda x: (x.astype(np.float32) * np.float32(1.0001)).astype(np.float32)  # not fp16 values
+    q, k, v = f(q), f(k), f(v)
+    o, s = _decode_run(dev, q, k, v, g, beta, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    _check(o, s, o_ref, s_ref, 2e-3, 1e-5, label="decode fp32 I/O")
+
+
 @pytest.mark.parametrize("kind", ["chunked", "recurrent"])
 @pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 100, 129])
 def test_ragged_and_head_map(dev, orc, kind, T):

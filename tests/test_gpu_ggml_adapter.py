@@ -1,13 +1,14 @@
 """GPU: tsa_ggml_gated_delta_net (the ggml-layout adapter) against the direct entry points
 and the oracle.
 
-The adapter only moves data (gathers strided / fp32 views into the kernels' dense fp16
-layout, scatters the output back) and dispatches on the tokens per sequence, so with input
-values that fp16 represents exactly its results must equal the direct entry point's bit for
-bit: tsa_gdn_decode_step (T = 1), tsa_gdn_recurrent_fwd (T < 32), tsa_gdn_chunked_fwd
-(T >= 32).  Cases: dense fp16 operands (used in place), fp32 views into a fused projection
-buffer with an fp32 strided output, a separate and a padded (non-dense) state_out, the
-dispatch boundary T = 31 / 32, and one case against the recurrence oracle with its gates.
+The adapter only moves data (gathers strided views into the kernels' dense layout, scatters
+the output back) and dispatches on the tokens per sequence and the operands' types, so its
+results must equal the direct entry point's bit for bit: tsa_gdn_decode_step (T = 1),
+tsa_gdn_recurrent_fwd (T < 32), tsa_gdn_chunked_fwd (T >= 32), or their *_f32 forms when any
+of q / k / v / out is fp32 (fp32 operands are never narrowed to fp16 in memory).  Cases:
+dense fp16 operands (used in place), fp32 views into a fused projection buffer with an fp32
+strided output, a separate and a padded (non-dense) state_out, the dispatch boundary T = 31
+/ 32, and one case against the recurrence oracle with its gates.
 """
 import numpy as np
 import pytest
@@ -34,9 +35,11 @@ def _t(dev, x):
     return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
 
 
-def _direct(dev, q, k, v, g, beta, st):
+def _direct(dev, q, k, v, g, beta, st, f32=False):
     import torch
     tq, tk, tv, tg, tb, ts = (_t(dev, x) for x in (q, k, v, g, beta, st))
+    if f32:  # the fp32-I/O entry points
+        tq, tk, tv = tq.float(), tk.float(), tv.float()
     T = q.shape[1]
     if T == 1:
         o = tsa.gdn_decode_step(tq[:, 0], tk[:, 0], tv[:, 0], tg[:, 0], tb[:, 0], ts)[:, None]
@@ -69,7 +72,8 @@ def test_fp32_views_of_a_fused_projection(dev, T):
     import torch
     B, Hk, Hv = 2, 2, 4
     q, k, v, g, beta, st = _data(np.random.default_rng(50 + T), B, T, Hk, Hv)
-    o_ref, s_ref = _direct(dev, q, k, v, g, beta, st)
+    o_ref, s_ref = _direct(dev, q, k, v, g, beta, st, f32=True)
+    o16, s16 = _direct(dev, q, k, v, g, beta, st)
     W = (2 * Hk + Hv) * D
     proj = torch.zeros(B, T, W, device=dev)
     proj[:, :, :Hk * D] = _t(dev, q).float().reshape(B, T, -1)
@@ -87,8 +91,11 @@ def test_fp32_views_of_a_fused_projection(dev, T):
     assert not qv.is_contiguous() and not out.is_contiguous()
     tsa.ggml_gated_delta_net(qv, kv, vv, gb[:, :, :Hv], gb[:, :, Hv:], ts_in, out, ts_out)
     torch.cuda.synchronize()
-    assert torch.equal(out.cpu(), o_ref.float())
+    assert out.dtype == torch.float32 and torch.equal(out.cpu(), o_ref)
     assert torch.equal(ts_out.cpu(), s_ref)
+    # the fp32 path on fp16-exact inputs carries the fp16 path's state bit for bit (its outputs
+    # may differ from the fp16 path's in the last rounding, tests/test_gpu_gdn.py covers that)
+    assert torch.equal(s_ref, s16)
     assert torch.equal(ts_in.cpu(), torch.from_numpy(st))        # input state untouched
     assert bool((outbuf[:, :, 1] == 7.0).all())                    # the gaps untouched
 

@@ -116,23 +116,46 @@ extern "C" int tsa_attn_gqa_naive(const void* q, const void* k, const void* v, c
 extern "C" size_t tsa_gdn_chunked_workspace_bytes(int B, int T, int Hq, int Hv, int dk, int dv,
                                                   int chunk) {
     if (B < 1 || T < 1 || Hq < 1 || Hv < 1 || dk != 128 || dv != 128 || chunk != 64) return 0;
-    return tsa::gdn_chunked_ws_bytes(B, T, Hv);
+    return tsa::gdn_chunked_ws_bytes(B, T, Hv, false);
 }
 
-extern "C" int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v,
-                                   const float* g_log, const float* beta, float* state, void* out,
-                                   int B, int T, int Hq, int Hv, int dk, int dv, int chunk,
-                                   float scale, void* ws, size_t ws_bytes, void* stream) {
+extern "C" size_t tsa_gdn_chunked_workspace_bytes_f32(int B, int T, int Hq, int Hv, int dk, int dv,
+                                                      int chunk) {
+    if (B < 1 || T < 1 || Hq < 1 || Hv < 1 || dk != 128 || dv != 128 || chunk != 64) return 0;
+    return tsa::gdn_chunked_ws_bytes(B, T, Hv, true);
+}
+
+namespace {
+int chunked(const void* q, const void* k, const void* v, const float* g_log, const float* beta,
+            float* state, void* out, int B, int T, int Hq, int Hv, int dk, int dv, int chunk,
+            float scale, void* ws, size_t ws_bytes, bool f32, void* stream) {
     int rc = check_gdn(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale);
     if (rc) return rc;
     if (chunk < 1) return TSA_ERR_SHAPE;
     if (dk != 128 || dv != 128 || chunk != 64) return TSA_ERR_UNSUPPORTED;
     const long long nch = (T + 63LL) / 64;
     if (!fits_int(B, Hv, nch) || !fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
-    const size_t need = tsa::gdn_chunked_ws_bytes(B, T, Hv);
+    const size_t need = tsa::gdn_chunked_ws_bytes(B, T, Hv, f32);
     if (!ws || ws_bytes < need) return TSA_ERR_WORKSPACE;
-    return from_hip(tsa::gdn_chunked(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale, ws,
+    return from_hip(tsa::gdn_chunked(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale, ws, f32,
                                      as_stream(stream)));
+}
+}  // namespace
+
+extern "C" int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v,
+                                   const float* g_log, const float* beta, float* state, void* out,
+                                   int B, int T, int Hq, int Hv, int dk, int dv, int chunk,
+                                   float scale, void* ws, size_t ws_bytes, void* stream) {
+    return chunked(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, chunk, scale, ws, ws_bytes,
+                   false, stream);
+}
+
+extern "C" int tsa_gdn_chunked_fwd_f32(const float* q, const float* k, const float* v,
+                                       const float* g_log, const float* beta, float* state, float* out,
+                                       int B, int T, int Hq, int Hv, int dk, int dv, int chunk,
+                                       float scale, void* ws, size_t ws_bytes, void* stream) {
+    return chunked(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, chunk, scale, ws, ws_bytes,
+                   true, stream);
 }
 
 extern "C" int tsa_gdn_chunked_fwd_noalloc(const void* q, const void* k, const void* v,
@@ -145,50 +168,84 @@ extern "C" int tsa_gdn_chunked_fwd_noalloc(const void* q, const void* k, const v
     if (dk != 128 || dv != 128 || chunk != 64) return TSA_ERR_UNSUPPORTED;
     const long long nch = (T + 63LL) / 64;
     if (!fits_int(B, Hv, nch) || !fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
-    if (tsa::gdn_chunked_ws_bytes(B, T, Hv) > tsa::gdn_chunked_noalloc_max_bytes()) return TSA_ERR_SCRATCH;
+    if (tsa::gdn_chunked_ws_bytes(B, T, Hv, false) > tsa::gdn_chunked_noalloc_max_bytes()) return TSA_ERR_SCRATCH;
     return from_hip(tsa::gdn_chunked_noalloc(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale,
                                              as_stream(stream)));
 }
 
 extern "C" int tsa_gdn_chunked_redo_count(const void* ws, size_t ws_bytes, int B, int T, int Hq,
-                                          int Hv, int dk, int dv, int chunk, int* count,
+                                          int Hv, int dk, int dv, int chunk, int io_f32, int* count,
                                           void* stream) {
     if (!ws || !count) return TSA_ERR_NULL;
     if (B < 1 || T < 1 || Hq < 1 || Hv < 1 || chunk < 1) return TSA_ERR_SHAPE;
     if (dk != 128 || dv != 128 || chunk != 64) return TSA_ERR_UNSUPPORTED;
+    if (io_f32 != 0 && io_f32 != 1) return TSA_ERR_ARG;
     const long long nch = (T + 63LL) / 64;
     if (!fits_int(B, Hv, nch) || !fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
-    if (ws_bytes < tsa::gdn_chunked_ws_bytes(B, T, Hv)) return TSA_ERR_WORKSPACE;
-    return from_hip(tsa::gdn_chunked_redo_count(ws, B, T, Hv, count, as_stream(stream)));
+    if (ws_bytes < tsa::gdn_chunked_ws_bytes(B, T, Hv, io_f32 != 0)) return TSA_ERR_WORKSPACE;
+    return from_hip(tsa::gdn_chunked_redo_count(ws, B, T, Hv, io_f32 != 0, count, as_stream(stream)));
 }
+
+namespace {
+int recurrent(const void* q, const void* k, const void* v, const float* g_log, const float* beta,
+              float* state, void* out, int B, int T, int Hq, int Hv, int dk, int dv, float scale,
+              bool f32, void* stream) {
+    int rc = check_gdn(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale);
+    if (rc) return rc;
+    if (dk != 128 || dv != 128) return TSA_ERR_UNSUPPORTED;
+    if (!fits_int(B, Hv, 4)) return TSA_ERR_SHAPE;
+    return from_hip(tsa::gdn_recurrent(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale, f32,
+                                       as_stream(stream)));
+}
+
+int naive(const void* q, const void* k, const void* v, const float* g_log, const float* beta,
+          float* state, void* out, int B, int T, int Hq, int Hv, int dk, int dv, float scale,
+          bool f32, void* stream) {
+    int rc = check_gdn(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale);
+    if (rc) return rc;
+    return from_hip(tsa::gdn_naive(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale, f32,
+                                   as_stream(stream)));
+}
+}  // namespace
 
 extern "C" int tsa_gdn_recurrent_fwd(const void* q, const void* k, const void* v,
                                      const float* g_log, const float* beta, float* state,
                                      void* out, int B, int T, int Hq, int Hv, int dk, int dv,
                                      float scale, void* stream) {
-    int rc = check_gdn(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale);
-    if (rc) return rc;
-    if (dk != 128 || dv != 128) return TSA_ERR_UNSUPPORTED;
-    if (!fits_int(B, Hv, 4)) return TSA_ERR_SHAPE;
-    return from_hip(tsa::gdn_recurrent(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale,
-                                       as_stream(stream)));
+    return recurrent(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale, false, stream);
+}
+
+extern "C" int tsa_gdn_recurrent_fwd_f32(const float* q, const float* k, const float* v,
+                                         const float* g_log, const float* beta, float* state,
+                                         float* out, int B, int T, int Hq, int Hv, int dk, int dv,
+                                         float scale, void* stream) {
+    return recurrent(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale, true, stream);
 }
 
 extern "C" int tsa_gdn_decode_step(const void* q, const void* k, const void* v,
                                    const float* g_log, const float* beta, float* state, void* out,
                                    int B, int Hq, int Hv, int dk, int dv, float scale,
                                    void* stream) {
-    return tsa_gdn_recurrent_fwd(q, k, v, g_log, beta, state, out, B, 1, Hq, Hv, dk, dv, scale,
-                                 stream);
+    return recurrent(q, k, v, g_log, beta, state, out, B, 1, Hq, Hv, dk, dv, scale, false, stream);
+}
+
+extern "C" int tsa_gdn_decode_step_f32(const float* q, const float* k, const float* v,
+                                       const float* g_log, const float* beta, float* state,
+                                       float* out, int B, int Hq, int Hv, int dk, int dv, float scale,
+                                       void* stream) {
+    return recurrent(q, k, v, g_log, beta, state, out, B, 1, Hq, Hv, dk, dv, scale, true, stream);
 }
 
 extern "C" int tsa_gdn_naive(const void* q, const void* k, const void* v, const float* g_log,
                              const float* beta, float* state, void* out, int B, int T, int Hq,
                              int Hv, int dk, int dv, float scale, void* stream) {
-    int rc = check_gdn(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale);
-    if (rc) return rc;
-    return from_hip(tsa::gdn_naive(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv,
-                                   scale, as_stream(stream)));
+    return naive(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale, false, stream);
+}
+
+extern "C" int tsa_gdn_naive_f32(const float* q, const float* k, const float* v, const float* g_log,
+                                 const float* beta, float* state, float* out, int B, int T, int Hq,
+                                 int Hv, int dk, int dv, float scale, void* stream) {
+    return naive(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale, true, stream);
 }
 
 extern "C" int tsa_gdn_chunked_fused_fwd(const void* q, const void* k, const void* v, const float* a,
@@ -204,7 +261,7 @@ extern "C" int tsa_gdn_chunked_fused_fwd(const void* q, const void* k, const voi
     if (dk != 128 || dv != 128 || chunk != 64) return TSA_ERR_UNSUPPORTED;
     const long long nch = (T + 63LL) / 64;
     if (!fits_int(B, Hv, nch) || !fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
-    const size_t need = tsa::gdn_chunked_ws_bytes(B, T, Hv);
+    const size_t need = tsa::gdn_chunked_ws_bytes(B, T, Hv, false);
     if (!ws || ws_bytes < need) return TSA_ERR_WORKSPACE;
     return from_hip(tsa::gdn_chunked_fused(q, k, v, tsa::GdnRawGates{a, b, dt_bias, A, eps}, state,
                                            out, B, T, Hq, Hv, scale, ws, as_stream(stream)));

@@ -52,6 +52,12 @@ constexpr int kWsAqk = kWsU + kC * kD * 4;  // fp16 [64 t][64]: column s stored 
 // qn_t, kn_t are the l2-norm factors of the fused entry point's raw q / k rows (1 otherwise)
 constexpr int kWsG = kWsAqk + kC * kC * 2;
 constexpr int kWsChunk = kWsG + kC * 16;    // 58368 B, multiple of 256
+// fp32 q / k / v / out (the reference's own I/O): the prep also leaves the chunk's K and Q
+// rows in fp16, unswizzled [64 t][128], for the carry's copies (LDS-DMA cannot convert)
+constexpr int kWsK = kWsChunk;
+constexpr int kWsQ = kWsK + kC * kD * 2;
+constexpr int kWsChunkF32 = kWsQ + kC * kD * 2;  // 91136 B
+template <bool kF32> constexpr int ws_chunk() { return kF32 ? kWsChunkF32 : kWsChunk; }
 
 // Ready flags, after all chunk workspaces: one word per (b, h, chunk), then an abort word per
 // carry workgroup.  Every call first clears them with a small kernel on the caller's stream
@@ -129,6 +135,16 @@ __device__ __forceinline__ void store_dev(float* p, float v) {
     asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
 
+// 8 consecutive q / k / v elements as 8 fp16 values (one uint4), from fp16 or fp32 memory:
+// fp32 inputs are converted in registers.
+__device__ __forceinline__ uint4 load8h(const half_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint4 load8h(const float* p) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    const half8_t h = {(half_t)a.x, (half_t)a.y, (half_t)a.z, (half_t)a.w,
+                       (half_t)b.x, (half_t)b.y, (half_t)b.z, (half_t)b.w};
+    return __builtin_bit_cast(uint4, h);
+}
+
 // ----------------------------------------------------------------------------------
 // Prep
 // ----------------------------------------------------------------------------------
@@ -166,10 +182,12 @@ struct PrepLds {
 // kFused: q / k are the raw rows (normalised here: the factors scale A, Aqk, W and the
 // workspace's e^G / e^{G_63 - G}, so the carry multiplies raw K / Q rows by them for free),
 // and g_log / beta are computed from the raw projections a / b (gate arguments).
-template <bool kFused>
+// TIO: the q / k / v element type (fp16, or fp32 with the K / Q rows left in fp16 in the
+// workspace for the carry).
+template <bool kFused, typename TIO>
 __global__ void __launch_bounds__(kThreads, 4)
-gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
-               const half_t* __restrict__ v, const float* __restrict__ g_log,
+gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
+               const TIO* __restrict__ v, const float* __restrict__ g_log,
                const float* __restrict__ beta, GdnRawGates gates, unsigned char* __restrict__ ws,
                unsigned* __restrict__ flags, int T, int Hq, int Hv, int nch, int BHv) {
     __shared__ PrepLds sm;
@@ -180,7 +198,8 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
     const int bh = blockIdx.x % BHv;
     const int b = bh / Hv, h = bh % Hv, hq = h % Hq;
     const int t0 = ch * kC;
-    unsigned char* wsc = ws + ((size_t)bh * nch + ch) * kWsChunk;
+    constexpr bool kF32 = std::is_same<TIO, float>::value;
+    unsigned char* wsc = ws + ((size_t)bh * nch + ch) * ws_chunk<kF32>();
     const int mt = wave >> 1, nt = wave & 1;  // this wave's 32x32 tile of K K^T / Q K^T
 
     // ---- 1. K rows to LDS, V rows and this wave's Q operand rows to registers ----
@@ -194,10 +213,11 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
         vreg[it] = kv;
         if (tt < T) {
             const size_t bt = (size_t)b * T + tt;
-            kv = *reinterpret_cast<const uint4*>(k + (bt * Hq + hq) * kD + c * 8);
-            vreg[it] = *reinterpret_cast<const uint4*>(v + (bt * Hv + h) * kD + c * 8);
+            kv = load8h(k + (bt * Hq + hq) * kD + c * 8);
+            vreg[it] = load8h(v + (bt * Hv + h) * kD + c * 8);
         }
         *reinterpret_cast<uint4*>(sm.K + tile_off(r, c)) = kv;
+        if (kF32) store_dev(wsc + kWsK + (size_t)(r * kD + c * 8) * 2, kv);
         if (kFused) {  // the row's 16 threads are 16 consecutive lanes of one wave
             const half8_t k8 = __builtin_bit_cast(half8_t, kv);
             float ss = 0.f;
@@ -213,10 +233,16 @@ gdn_chunk_prep(const half_t* __restrict__ q, const half_t* __restrict__ k,
     half8_t qa[kD / 16];
     {
         const int tt = t0 + 32 * mt + (lane & 31);
-        const half_t* qrow = q + (((size_t)b * T + tt) * Hq + hq) * kD + 8 * hi;
+        const TIO* qrow = q + (((size_t)b * T + tt) * Hq + hq) * kD + 8 * hi;
 #pragma unroll
         for (int s = 0; s < kD / 16; ++s)
-            qa[s] = tt < T ? *reinterpret_cast<const half8_t*>(qrow + 16 * s) : half8_t{};
+            qa[s] = tt < T ? __builtin_bit_cast(half8_t, load8h(qrow + 16 * s)) : half8_t{};
+        if (kF32 && nt == 0) {  // waves 0 and 2 hold the chunk's 64 Q rows
+            const int row = 32 * mt + (lane & 31);
+#pragma unroll
+            for (int s = 0; s < kD / 16; ++s)
+                store_dev(wsc + kWsQ + (size_t)(row * kD + 16 * s + 8 * hi) * 2, __builtin_bit_cast(uint4, qa[s]));
+        }
         if (kFused) {  // the two halves of the row are lanes l and l ^ 32
             float ss = 0.f;
 #pragma unroll
@@ -561,11 +587,15 @@ __device__ __forceinline__ void dma_wait_barrier() {
 // operands of chunk it+1 into cs[(it+1)&1] and the output operands of chunk it into
 // os[it&1] (the prologue: chunk 0 into cs[0]), then waits for them and meets the barrier.
 // A chunk that ends past T recomputes its K / Q offsets with clamped rows.
-template <int W>
+// kh / qh: the K / Q rows of chunk 0 (the inputs' rows, or with kF32 the fp16 copies in the
+// workspace, which the prep writes in this call and are therefore read device-scope), with
+// rowbytes between rows and chunk_bytes between chunks.
+template <int W, bool kF32>
 __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const unsigned char* kh,
                                          const unsigned char* qh, const unsigned char* wsh,
                                          const unsigned* fl, unsigned wait_ticks,
-                                         int* err, unsigned rowbytes, int pair, int T, int nch) {
+                                         int* err, unsigned rowbytes, size_t chunk_bytes, int pair,
+                                         int T, int nch) {
     constexpr int kJ = (kDmaN - W + 3) / 4;
     const int lane = threadIdx.x & 63;
     unsigned off[kJ];
@@ -575,10 +605,10 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
     auto copies = [&](int pc, int po, int cn, int co) {
         const bool do_c = cn < nch, do_o = co >= 0 && co < nch;
         const int last_c = min(kC - 1, T - 1 - cn * kC), last_o = min(kC - 1, T - 1 - co * kC);
-        const unsigned char* kb = kh + (size_t)cn * kC * rowbytes;
-        const unsigned char* wc = wsh + (size_t)cn * kWsChunk;
-        const unsigned char* qb = qh + (size_t)co * kC * rowbytes;
-        const unsigned char* wo = wsh + (size_t)co * kWsChunk;
+        const unsigned char* kb = kh + (size_t)cn * chunk_bytes;
+        const unsigned char* wc = wsh + (size_t)cn * ws_chunk<kF32>();
+        const unsigned char* qb = qh + (size_t)co * chunk_bytes;
+        const unsigned char* wo = wsh + (size_t)co * ws_chunk<kF32>();
         auto issue_all = [&](auto Ragged) {
 #pragma unroll
             for (int j = 0; j < kJ; ++j) {
@@ -592,7 +622,7 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
                     o = dma_src_off(n, lane, rowbytes, pair, chainslot ? last_c : last_o);
                 const unsigned char* base = chainslot ? (rows ? kb : wc) : (rows ? qb : wo);
                 const unsigned lds = (chainslot ? slot_lds[pc] : slot_lds[2 + po]) + 1024u * i;
-                dma_issue(base, o, lds, n == kDmaEOut, !rows);
+                dma_issue(base, o, lds, n == kDmaEOut, kF32 || !rows);
             }
         };
         if ((do_c && last_c < kC - 1) || (do_o && last_o < kC - 1))
@@ -740,8 +770,12 @@ __device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs
 }
 
 // Output for one chunk, token tiles {2w, 2w+1} of both strips: O = scale (e^G Q S + Aqk Vnew).
+// With TIO = float the values go straight to the fp32 output (o32: this wave's first token
+// row of the chunk and the workgroup's first column; rows past T are skipped) instead of
+// through the fp16 staging tile.
+template <typename TIO>
 __device__ __forceinline__ void out_step(const OutSlot& os, const uint4 (*xs)[6][64], half_t* ostage,
-                                         int w, float scale) {
+                                         int w, float scale, float* o32, size_t o32_row, int rows_left) {
     const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
     half8_t aQ[2][4], aA[2][2];
     float eg[2][4];
@@ -784,6 +818,19 @@ __device__ __forceinline__ void out_step(const OutSlot& os, const uint4 (*xs)[6]
             for (int ks = 0; ks < 2; ++ks) av[j][s] = mfma16(aA[j][ks], Vn[s][ks], av[j][s]);
         }
     }
+    if (std::is_same<TIO, float>::value) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tl = 16 * j + 4 * g + r;  // token within this wave's 32
+                if (tl < rows_left)
+#pragma unroll
+                    for (int s = 0; s < kStrips; ++s)
+                        o32[tl * o32_row + 16 * s + c] = scale * fmaf(eg[j][r], qs[j][s][r], av[j][s][r]);
+            }
+        return;
+    }
     // O tile (32 tokens x 32 columns) staged in LDS; out_flush stores it
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -813,12 +860,16 @@ __device__ __forceinline__ void out_flush(const half_t* ostage, half_t* out, int
     wave_lds_sync();
 }
 
+// TIO: the q / k / out element type.  With fp32 I/O the K / Q rows come from the prep's fp16
+// copies in the workspace and the output is stored in fp32 straight from registers.
+template <typename TIO>
 __global__ void __launch_bounds__(kCarryThreads, 1)
-gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
+gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
                 const unsigned char* __restrict__ ws, const unsigned* __restrict__ flags,
                 unsigned* __restrict__ aborts, int mode, unsigned wait_ticks,
                 float* __restrict__ state,
-                half_t* __restrict__ out, int T, int Hq, int Hv, int nch, int BHv, float scale) {
+                TIO* __restrict__ out, int T, int Hq, int Hv, int nch, int BHv, float scale) {
+    constexpr bool kF32 = std::is_same<TIO, float>::value;
     __shared__ CarryLds sm;
     if (mode == kCarryRetry &&
         __builtin_amdgcn_readfirstlane(__hip_atomic_load(aborts + blockIdx.x, __ATOMIC_RELAXED,
@@ -831,7 +882,7 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
     const int pair = blockIdx.x / BHv;
     const int bh = blockIdx.x % BHv;
     const int b = bh / Hv, h = bh % Hv, hq = h % Hq;
-    const unsigned char* wsh = ws + (size_t)bh * nch * kWsChunk;
+    const unsigned char* wsh = ws + (size_t)bh * nch * ws_chunk<kF32>();
     const bool chain = wave < 2, outw = wave == 2 || wave == 3, dmaw = wave >= 4;
     const int sl = wave & 1;  // chain wave: its strip; output wave: w = wave - 2
 
@@ -864,19 +915,31 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
         }
     } else if (outw) {
         const int w = wave - 2;
+        half_t* out16 = reinterpret_cast<half_t*>(out);
+        // fp32 output: row of token t0 + 32 w of chunk ch, column pair * 32
+        const size_t orow = (size_t)Hv * kD;
+        float* o32 = reinterpret_cast<float*>(out) + ((size_t)b * T + 32 * w) * orow + (size_t)h * kD + pair * 32;
+        auto step = [&](int slot, int ch) {
+            out_step<TIO>(sm.os[slot], sm.XS[slot], sm.OS[w], w, scale, o32 + (size_t)ch * kC * orow, orow,
+                          T - ch * kC - 32 * w);
+        };
         for (int it = 0; it <= nch; it += 2) {
-            if (it >= 2) out_flush(sm.OS[w], out, b, T, Hv, h, (it - 2) * kC, pair, w);
-            if (it >= 1) out_step(sm.os[1], sm.XS[1], sm.OS[w], w, scale);
+            if (!kF32 && it >= 2) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 2) * kC, pair, w);
+            if (it >= 1) step(1, it - 1);
             lds_barrier();  // the O stores need not complete before the barrier
             if (it + 1 > nch) break;
-            if (it >= 1) out_flush(sm.OS[w], out, b, T, Hv, h, (it - 1) * kC, pair, w);
-            out_step(sm.os[0], sm.XS[0], sm.OS[w], w, scale);
+            if (!kF32 && it >= 1) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 1) * kC, pair, w);
+            step(0, it);
             lds_barrier();
         }
     } else {
-        const unsigned rowbytes = (unsigned)Hq * kD * 2;
-        const unsigned char* kh = reinterpret_cast<const unsigned char*>(k + ((size_t)b * T * Hq + hq) * kD);
-        const unsigned char* qh = reinterpret_cast<const unsigned char*>(q + ((size_t)b * T * Hq + hq) * kD);
+        // the inputs' K / Q rows, or with fp32 I/O the prep's fp16 copies in the workspace
+        const unsigned rowbytes = kF32 ? (unsigned)kD * 2 : (unsigned)Hq * kD * 2;
+        const size_t chunk_bytes = kF32 ? (size_t)kWsChunkF32 : (size_t)kC * rowbytes;
+        const unsigned char* kh = kF32 ? wsh + kWsK
+                                       : reinterpret_cast<const unsigned char*>(k + ((size_t)b * T * Hq + hq) * kD);
+        const unsigned char* qh = kF32 ? wsh + kWsQ
+                                       : reinterpret_cast<const unsigned char*>(q + ((size_t)b * T * Hq + hq) * kD);
         const unsigned slot_lds[4] = {(unsigned)(uintptr_t)(lds_void_t)(void*)&sm.cs[0],
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.cs[1],
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.os[0],
@@ -884,10 +947,10 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
         const unsigned* fl = flags + (size_t)bh * nch;
         int* err = &sm.err[wave - 4];
         switch (wave) {
-            case 4: dma_role<0>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, pair, T, nch); break;
-            case 5: dma_role<1>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, pair, T, nch); break;
-            case 6: dma_role<2>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, pair, T, nch); break;
-            default: dma_role<3>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, pair, T, nch); break;
+            case 4: dma_role<0, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, T, nch); break;
+            case 5: dma_role<1, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, T, nch); break;
+            case 6: dma_role<2, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, T, nch); break;
+            default: dma_role<3, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, T, nch); break;
         }
     }
     if (chain) {
@@ -906,8 +969,8 @@ gdn_chunk_carry(const half_t* __restrict__ q, const half_t* __restrict__ k,
                 *reinterpret_cast<float4*>(Sg + 16 * m + 4 * g) =
                     lost ? make_float4(nan, nan, nan, nan) : make_float4(S[m][0], S[m][1], S[m][2], S[m][3]);
         }
-    } else if (outw) {
-        out_flush(sm.OS[wave - 2], out, b, T, Hv, h, (nch - 1) * kC, pair, wave - 2);
+    } else if (outw && !kF32) {
+        out_flush(sm.OS[wave - 2], reinterpret_cast<half_t*>(out), b, T, Hv, h, (nch - 1) * kC, pair, wave - 2);
     }
 }
 
@@ -919,10 +982,10 @@ __global__ void __launch_bounds__(256) gdn_flags_clear(unsigned* __restrict__ w,
 
 }  // namespace
 
-size_t gdn_chunked_ws_bytes(int B, int T, int Hv) {
+size_t gdn_chunked_ws_bytes(int B, int T, int Hv, bool f32) {
     const size_t nch = (size_t)(T + kC - 1) / kC;
     // chunk workspaces, then a ready flag per chunk, then an abort word per carry workgroup
-    return (size_t)B * Hv * nch * (kWsChunk + sizeof(unsigned)) +
+    return (size_t)B * Hv * nch * ((f32 ? kWsChunkF32 : kWsChunk) + sizeof(unsigned)) +
            (size_t)B * Hv * (kD / (16 * kStrips)) * sizeof(unsigned);
 }
 
@@ -960,7 +1023,7 @@ unsigned carry_wait_ticks() { return (unsigned)(env_long("TSA_GDN_CARRY_WAIT_US"
 // would otherwise wait out the carry's time limit before its second launch.
 bool overlap_allowed() { return env_long("TSA_GDN_OVERLAP", 1, 1) != 0; }
 
-template <bool kFused>
+template <bool kFused, typename TIO>
 hipError_t launch_chunked(const void* q, const void* k, const void* v, const float* g_log,
                           const float* beta, const GdnRawGates& gates, float* state, void* out,
                           int B, int T, int Hq, int Hv, float scale, void* ws, bool may_overlap,
@@ -968,10 +1031,10 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
     const int nch = (T + kC - 1) / kC;
     const int BHv = B * Hv;
     const int carry_wgs = BHv * (kD / (16 * kStrips));
-    auto Q = static_cast<const half_t*>(q);
-    auto K = static_cast<const half_t*>(k);
+    auto Q = static_cast<const TIO*>(q);
+    auto K = static_cast<const TIO*>(k);
     auto W = static_cast<unsigned char*>(ws);
-    unsigned* flags = reinterpret_cast<unsigned*>(W + (size_t)BHv * nch * kWsChunk);
+    unsigned* flags = reinterpret_cast<unsigned*>(W + (size_t)BHv * nch * ws_chunk<std::is_same<TIO, float>::value>());
     unsigned* aborts = flags + (size_t)BHv * nch;
     const int nflags = BHv * nch + carry_wgs;
     const unsigned wait_ticks = carry_wait_ticks();
@@ -980,14 +1043,14 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
         return hipGetLastError();
     };
     auto prep = [&](hipStream_t st) {
-        hipLaunchKernelGGL(gdn_chunk_prep<kFused>, dim3(BHv * nch), dim3(kThreads), 0, st, Q, K,
-                           static_cast<const half_t*>(v), g_log, beta, gates, W, flags, T, Hq, Hv,
+        hipLaunchKernelGGL((gdn_chunk_prep<kFused, TIO>), dim3(BHv * nch), dim3(kThreads), 0, st, Q, K,
+                           static_cast<const TIO*>(v), g_log, beta, gates, W, flags, T, Hq, Hv,
                            nch, BHv);
         return hipGetLastError();
     };
     auto carry = [&](int mode, unsigned ticks) {
-        hipLaunchKernelGGL(gdn_chunk_carry, dim3(carry_wgs), dim3(kCarryThreads), 0, stream, Q, K, W,
-                           flags, aborts, mode, ticks, state, static_cast<half_t*>(out), T, Hq, Hv,
+        hipLaunchKernelGGL(gdn_chunk_carry<TIO>, dim3(carry_wgs), dim3(kCarryThreads), 0, stream, Q, K, W,
+                           flags, aborts, mode, ticks, state, static_cast<TIO*>(out), T, Hq, Hv,
                            nch, BHv, scale);
         return hipGetLastError();
     };
@@ -1090,15 +1153,16 @@ hipError_t gdn_chunked_noalloc(const void* q, const void* k, const void* v, cons
     const hipError_t e = scratch_address(stream, &ws);
     if (e != hipSuccess) return e;
     // in order on the caller's stream: no side stream or event is ever created here
-    return launch_chunked<false>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq, Hv,
-                                 scale, ws, false, stream);
+    return launch_chunked<false, half_t>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq, Hv,
+                                         scale, ws, false, stream);
 }
 
-hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, int* count, hipStream_t stream) {
+hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, bool f32, int* count,
+                                  hipStream_t stream) {
     const size_t nch = (size_t)(T + kC - 1) / kC;
     const size_t n = (size_t)B * Hv * (kD / (16 * kStrips));
     const unsigned char* aborts = static_cast<const unsigned char*>(ws) +
-                                  (size_t)B * Hv * nch * (kWsChunk + sizeof(unsigned));
+                                  (size_t)B * Hv * nch * ((f32 ? kWsChunkF32 : kWsChunk) + sizeof(unsigned));
     unsigned* host = static_cast<unsigned*>(std::malloc(n * sizeof(unsigned)));
     if (!host) return hipErrorOutOfMemory;
     hipError_t e = hipMemcpyAsync(host, aborts, n * sizeof(unsigned), hipMemcpyDeviceToHost, stream);
@@ -1114,16 +1178,19 @@ hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, int* cou
 
 hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,
                        const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
-                       float scale, void* ws, hipStream_t stream) {
-    return launch_chunked<false>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq, Hv,
-                                 scale, ws, true, stream);
+                       float scale, void* ws, bool f32, hipStream_t stream) {
+    if (f32)
+        return launch_chunked<false, float>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq,
+                                            Hv, scale, ws, true, stream);
+    return launch_chunked<false, half_t>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq, Hv,
+                                         scale, ws, true, stream);
 }
 
 hipError_t gdn_chunked_fused(const void* q, const void* k, const void* v, const GdnRawGates& gates,
                              float* state, void* out, int B, int T, int Hq, int Hv, float scale,
                              void* ws, hipStream_t stream) {
-    return launch_chunked<true>(q, k, v, nullptr, nullptr, gates, state, out, B, T, Hq, Hv, scale,
-                                ws, true, stream);
+    return launch_chunked<true, half_t>(q, k, v, nullptr, nullptr, gates, state, out, B, T, Hq, Hv,
+                                        scale, ws, true, stream);
 }
 
 }  // namespace tsa

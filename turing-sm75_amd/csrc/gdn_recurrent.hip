@@ -20,6 +20,8 @@
 // The reference's token-serial family (serial/smem/occ/occ2/occ4/occ4p/occ8,
 // src/gdn_sm75.cu:57-188,577-893) differs only in how many columns a warp owns; here the
 // state stays fp32 (gdn_smem_kernel's fp16 state is not reproduced).
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -33,23 +35,33 @@ constexpr int kBlocksPerHead = kD / kColsPerBlock;
 constexpr int kDecodeCols = 8;  // decode: columns per workgroup
 constexpr int kDecodeLpc = 8;   // decode: lanes per column
 
-__device__ __forceinline__ void load_row16(const half_t* __restrict__ p, int j, float (&x)[16]) {
+// q / k / v / out are fp16 (TIO = half_t, the library's I/O type) or fp32 (TIO = float, the
+// reference's own, src/gdn_sm75.cu:57-64): 4 consecutive elements as fp32 either way.
+__device__ __forceinline__ float4_t load4(const half_t* p) {
+    const half4_t h = *reinterpret_cast<const half4_t*>(p);
+    return float4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+__device__ __forceinline__ float4_t load4(const float* p) { return *reinterpret_cast<const float4_t*>(p); }
+
+template <typename TIO>
+__device__ __forceinline__ void load_row16(const TIO* __restrict__ p, int j, float (&x)[16]) {
     // rows 4*(it*8 + j) .. +3 for it = 0..3
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-        const half4_t h = *reinterpret_cast<const half4_t*>(p + 4 * (it * 8 + j));
-        x[4 * it + 0] = (float)h[0];
-        x[4 * it + 1] = (float)h[1];
-        x[4 * it + 2] = (float)h[2];
-        x[4 * it + 3] = (float)h[3];
+        const float4_t h = load4(p + 4 * (it * 8 + j));
+        x[4 * it + 0] = h[0];
+        x[4 * it + 1] = h[1];
+        x[4 * it + 2] = h[2];
+        x[4 * it + 3] = h[3];
     }
 }
 
+template <typename TIO>
 __global__ void __launch_bounds__(kThreads)
-gdn_recurrent_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
-                     const half_t* __restrict__ v, const float* __restrict__ g_log,
+gdn_recurrent_kernel(const TIO* __restrict__ q, const TIO* __restrict__ k,
+                     const TIO* __restrict__ v, const float* __restrict__ g_log,
                      const float* __restrict__ beta, float* __restrict__ state,
-                     half_t* __restrict__ out, int T, int Hq, int Hv, float scale) {
+                     TIO* __restrict__ out, int T, int Hq, int Hv, float scale) {
     const int bh = blockIdx.x / kBlocksPerHead;
     const int cb = blockIdx.x % kBlocksPerHead;
     const int b = bh / Hv, h = bh % Hv, hq = h % Hq;
@@ -96,7 +108,7 @@ gdn_recurrent_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
             s[it][2] = fmaf(g, s[it][2], kr[4 * it + 2] * d);
             s[it][3] = fmaf(g, s[it][3], kr[4 * it + 3] * d);
         }
-        if (j == 0) out[(bt * Hv + h) * kD + col] = (half_t)(scale * fmaf(g, sq, d * kq));
+        if (j == 0) out[(bt * Hv + h) * kD + col] = (TIO)(scale * fmaf(g, sq, d * kq));
     }
 #pragma unroll
     for (int it = 0; it < 4; ++it) __builtin_nontemporal_store(s[it], Sc + it * 8 + j);
@@ -123,12 +135,12 @@ __device__ __forceinline__ float sum_lanes(float x) {
 // nothing.  kFused: q / k are raw rows, normalised here (their norms come from the same
 // lane-group sums as the dot products), and g_log / beta come from the raw projections
 // a / b (gate arguments).
-template <int kCols, int kLpc, bool kFused>
+template <int kCols, int kLpc, bool kFused, typename TIO>
 __global__ void __launch_bounds__(kLpc * kCols)
-gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
-                  const half_t* __restrict__ v, const float* __restrict__ g_log,
+gdn_decode_kernel(const TIO* __restrict__ q, const TIO* __restrict__ k,
+                  const TIO* __restrict__ v, const float* __restrict__ g_log,
                   const float* __restrict__ beta, GdnRawGates gates, float* __restrict__ state,
-                  half_t* __restrict__ out, int Hq, int Hv, float scale) {
+                  TIO* __restrict__ out, int Hq, int Hv, float scale) {
     static_assert(kLpc * kCols >= 64, "wave 0 loads the q / k rows");
     constexpr int kWgPerHead = kD / kCols;
     constexpr int kR = 32 / kLpc;  // float4 chunks of the column per lane
@@ -139,7 +151,8 @@ gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
     const size_t bt = (size_t)b;  // token index of sequence b (T = 1)
     const size_t vrow = (bt * Hv + h) * kD;
 
-    __shared__ half4_t kq_rows[2][kD / 4];
+    typedef typename std::conditional<std::is_same<TIO, float>::value, float4_t, half4_t>::type row4_t;
+    __shared__ row4_t kq_rows[2][kD / 4];
     float4_t* Sc = reinterpret_cast<float4_t*>(state + ((size_t)bh * kD + col) * kD);
     float4_t s[kR];
 #pragma unroll
@@ -151,9 +164,9 @@ gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt left at their maxima
     __builtin_amdgcn_sched_barrier(0);
-    if (tid < 64) {  // wave 0 -- lanes 0-31: k row, 32-63: q row, 4 halfs each
-        const half_t* row = (tid < 32 ? k : q) + (bt * Hq + hq) * kD;
-        kq_rows[tid >> 5][tid & 31] = *reinterpret_cast<const half4_t*>(row + 4 * (tid & 31));
+    if (tid < 64) {  // wave 0 -- lanes 0-31: k row, 32-63: q row, 4 elements each
+        const TIO* row = (tid < 32 ? k : q) + (bt * Hq + hq) * kD;
+        kq_rows[tid >> 5][tid & 31] = *reinterpret_cast<const row4_t*>(row + 4 * (tid & 31));
     }
     const float vc = (float)v[vrow + col];
     float g, be;
@@ -168,7 +181,7 @@ gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
     float kr[4 * kR], qr[4 * kR];
 #pragma unroll
     for (int it = 0; it < kR; ++it) {
-        const half4_t hk = kq_rows[0][it * kLpc + j], hq4 = kq_rows[1][it * kLpc + j];
+        const row4_t hk = kq_rows[0][it * kLpc + j], hq4 = kq_rows[1][it * kLpc + j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             kr[4 * it + e] = (float)hk[e];
@@ -211,15 +224,16 @@ gdn_decode_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
         for (int e = 0; e < 4; ++e) x[e] = fmaf(g, s[it][e], kr[4 * it + e] * d);
         __builtin_nontemporal_store(x, Sc + it * kLpc + j);
     }
-    if (j == 0) out[vrow + col] = (half_t)(scale * fmaf(g, sq, d * kq));
+    if (j == 0) out[vrow + col] = (TIO)(scale * fmaf(g, sq, d * kq));
 }
 
 // Naive check kernel: one thread per state column, gdn_cpu order (src/gdn_sm75.cu:1090-1102).
+template <typename TIO>
 __global__ void __launch_bounds__(128)
-gdn_naive_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
-                 const half_t* __restrict__ v, const float* __restrict__ g_log,
+gdn_naive_kernel(const TIO* __restrict__ q, const TIO* __restrict__ k,
+                 const TIO* __restrict__ v, const float* __restrict__ g_log,
                  const float* __restrict__ beta, float* __restrict__ state,
-                 half_t* __restrict__ out, int B, int T, int Hq, int Hv, int dk, int dv,
+                 TIO* __restrict__ out, int B, int T, int Hq, int Hv, int dk, int dv,
                  float scale) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (long long)B * Hv * dv) return;
@@ -229,8 +243,8 @@ gdn_naive_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
     float* Sc = state + ((size_t)bh * dv + c) * dk;
     for (int t = 0; t < T; ++t) {
         const size_t bt = (size_t)b * T + t;
-        const half_t* qt = q + (bt * Hq + hq) * dk;
-        const half_t* kt = k + (bt * Hq + hq) * dk;
+        const TIO* qt = q + (bt * Hq + hq) * dk;
+        const TIO* kt = k + (bt * Hq + hq) * dk;
         const float g = expf(g_log[bt * Hv + h]);
         const float be = beta[bt * Hv + h];
         float kv = 0.f;
@@ -242,52 +256,69 @@ gdn_naive_kernel(const half_t* __restrict__ q, const half_t* __restrict__ k,
             Sc[i] = sn;
             attn += sn * (float)qt[i];
         }
-        out[(bt * Hv + h) * dv + c] = (half_t)(attn * scale);
+        out[(bt * Hv + h) * dv + c] = (TIO)(attn * scale);
     }
+}
+
+template <typename TIO>
+hipError_t launch_recurrent(const void* q, const void* k, const void* v, const float* g_log,
+                            const float* beta, float* state, void* out, int B, int T, int Hq,
+                            int Hv, float scale, hipStream_t stream) {
+    auto Q = static_cast<const TIO*>(q);
+    auto K = static_cast<const TIO*>(k);
+    auto V = static_cast<const TIO*>(v);
+    auto O = static_cast<TIO*>(out);
+    if (T == 1) {
+        const unsigned blocks = (unsigned)(B * Hv * (kD / kDecodeCols));
+        hipLaunchKernelGGL((gdn_decode_kernel<kDecodeCols, kDecodeLpc, false, TIO>), dim3(blocks),
+                           dim3(kDecodeLpc * kDecodeCols), 0, stream, Q, K, V, g_log, beta,
+                           GdnRawGates{}, state, O, Hq, Hv, scale);
+        return hipGetLastError();
+    }
+    const unsigned blocks = (unsigned)(B * Hv * kBlocksPerHead);
+    hipLaunchKernelGGL(gdn_recurrent_kernel<TIO>, dim3(blocks), dim3(kThreads), 0, stream, Q, K, V,
+                       g_log, beta, state, O, T, Hq, Hv, scale);
+    return hipGetLastError();
+}
+
+template <typename TIO>
+hipError_t launch_naive(const void* q, const void* k, const void* v, const float* g_log,
+                        const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
+                        int dk, int dv, float scale, hipStream_t stream) {
+    const long long cols = (long long)B * Hv * dv;
+    const unsigned blocks = (unsigned)((cols + 127) / 128);
+    hipLaunchKernelGGL(gdn_naive_kernel<TIO>, dim3(blocks), dim3(128), 0, stream,
+                       static_cast<const TIO*>(q), static_cast<const TIO*>(k),
+                       static_cast<const TIO*>(v), g_log, beta, state, static_cast<TIO*>(out), B, T,
+                       Hq, Hv, dk, dv, scale);
+    return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t gdn_recurrent(const void* q, const void* k, const void* v, const float* g_log,
                          const float* beta, float* state, void* out, int B, int T, int Hq,
-                         int Hv, float scale, hipStream_t stream) {
-    if (T == 1) {
-        const unsigned blocks = (unsigned)(B * Hv * (kD / kDecodeCols));
-        hipLaunchKernelGGL((gdn_decode_kernel<kDecodeCols, kDecodeLpc, false>), dim3(blocks), dim3(kDecodeLpc * kDecodeCols),
-                           0, stream, static_cast<const half_t*>(q), static_cast<const half_t*>(k),
-                           static_cast<const half_t*>(v), g_log, beta, GdnRawGates{}, state,
-                           static_cast<half_t*>(out), Hq, Hv, scale);
-        return hipGetLastError();
-    }
-    const unsigned blocks = (unsigned)(B * Hv * kBlocksPerHead);
-    hipLaunchKernelGGL(gdn_recurrent_kernel, dim3(blocks), dim3(kThreads), 0, stream,
-                       static_cast<const half_t*>(q), static_cast<const half_t*>(k),
-                       static_cast<const half_t*>(v), g_log, beta, state,
-                       static_cast<half_t*>(out), T, Hq, Hv, scale);
-    return hipGetLastError();
+                         int Hv, float scale, bool f32, hipStream_t stream) {
+    return f32 ? launch_recurrent<float>(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale, stream)
+               : launch_recurrent<half_t>(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale, stream);
 }
 
 hipError_t gdn_decode_fused(const void* q, const void* k, const void* v, const GdnRawGates& gates,
                             float* state, void* out, int B, int Hq, int Hv, float scale,
                             hipStream_t stream) {
     const unsigned blocks = (unsigned)(B * Hv * (kD / kDecodeCols));
-    hipLaunchKernelGGL((gdn_decode_kernel<kDecodeCols, kDecodeLpc, true>), dim3(blocks), dim3(kDecodeLpc * kDecodeCols), 0,
-                       stream, static_cast<const half_t*>(q), static_cast<const half_t*>(k),
-                       static_cast<const half_t*>(v), nullptr, nullptr, gates, state,
-                       static_cast<half_t*>(out), Hq, Hv, scale);
+    hipLaunchKernelGGL((gdn_decode_kernel<kDecodeCols, kDecodeLpc, true, half_t>), dim3(blocks),
+                       dim3(kDecodeLpc * kDecodeCols), 0, stream, static_cast<const half_t*>(q),
+                       static_cast<const half_t*>(k), static_cast<const half_t*>(v), nullptr, nullptr,
+                       gates, state, static_cast<half_t*>(out), Hq, Hv, scale);
     return hipGetLastError();
 }
 
 hipError_t gdn_naive(const void* q, const void* k, const void* v, const float* g_log,
                      const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
-                     int dk, int dv, float scale, hipStream_t stream) {
-    const long long cols = (long long)B * Hv * dv;
-    const unsigned blocks = (unsigned)((cols + 127) / 128);
-    hipLaunchKernelGGL(gdn_naive_kernel, dim3(blocks), dim3(128), 0, stream,
-                       static_cast<const half_t*>(q), static_cast<const half_t*>(k),
-                       static_cast<const half_t*>(v), g_log, beta, state,
-                       static_cast<half_t*>(out), B, T, Hq, Hv, dk, dv, scale);
-    return hipGetLastError();
+                     int dk, int dv, float scale, bool f32, hipStream_t stream) {
+    return f32 ? launch_naive<float>(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale, stream)
+               : launch_naive<half_t>(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale, stream);
 }
 
 }  // namespace tsa

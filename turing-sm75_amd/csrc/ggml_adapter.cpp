@@ -9,8 +9,10 @@
 //   state, state_out  [S, S, Hv, B]  (ne[0] = the k index: S[b][h][c][i], the reference's
 //                                     [Hv][dv][dk] state per sequence, src/gdn_sm75.cu:71-72)
 // with S = 128.  q / k / v / out may be fp32 (ggml's op) or fp16 and any strides (views
-// into a fused projection); g_log, beta and the states are fp32.  Operands already in the
-// kernels' dense fp16 / fp32 layout are used in place; the others are gathered into the
+// into a fused projection); g_log, beta and the states are fp32.  When any of q / k / v / out
+// is fp32 the kernels run with fp32 I/O (fp16 operands are widened, exactly), so fp32
+// operands are never narrowed; when all four are fp16 they run with fp16 I/O.  Operands
+// already in the kernels' dense layout are used in place; the others are gathered into the
 // caller's workspace (and the output scattered back) by strided copy kernels.  state_out
 // may be the same buffer as state (in place).
 //
@@ -67,17 +69,18 @@ bool same_ne(const tsa_tensor& t, int64_t a, int64_t b, int64_t c, int64_t d) {
     return t.ne[0] == a && t.ne[1] == b && t.ne[2] == c && t.ne[3] == d;
 }
 
-// Workspace layout: dense fp16 q, k, v, out; dense fp32 g_log, beta, state; the chunked
-// prefill's workspace.  Each piece is 256-byte aligned and sized for the worst case (every
-// operand copied), so the size depends on the shapes only.
+// Workspace layout: dense q, k, v, out in the I/O type (fp16, or fp32 when f32); dense fp32
+// g_log, beta, state; the chunked prefill's workspace.  Each piece is 256-byte aligned and
+// sized for the worst case (every operand copied), so the size depends on the shapes only.
 struct Plan {
     int64_t B, T, Hk, Hv;
     size_t q, k, v, out, g, beta, state, chunk, total;
 };
 
-Plan plan(int64_t B, int64_t T, int64_t Hk, int64_t Hv) {
+Plan plan(int64_t B, int64_t T, int64_t Hk, int64_t Hv, bool f32) {
     Plan p{B, T, Hk, Hv, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    const size_t qk = (size_t)(B * T * Hk * kS) * 2, vo = (size_t)(B * T * Hv * kS) * 2;
+    const size_t e = f32 ? 4 : 2;
+    const size_t qk = (size_t)(B * T * Hk * kS) * e, vo = (size_t)(B * T * Hv * kS) * e;
     const size_t gb = (size_t)(B * T * Hv) * 4, st = (size_t)(B * Hv * kS * kS) * 4;
     size_t off = 0;
     p.q = off;     off += align256(qk);
@@ -88,7 +91,7 @@ Plan plan(int64_t B, int64_t T, int64_t Hk, int64_t Hv) {
     p.beta = off;  off += align256(gb);
     p.state = off; off += align256(st);
     p.chunk = off;
-    if (T >= kChunkedMinT) off += tsa::gdn_chunked_ws_bytes((int)B, (int)T, (int)Hv);
+    if (T >= kChunkedMinT) off += tsa::gdn_chunked_ws_bytes((int)B, (int)T, (int)Hv, f32);
     p.total = off;
     return p;
 }
@@ -136,7 +139,8 @@ extern "C" size_t tsa_ggml_gdn_workspace_bytes(const tsa_tensor* q, const tsa_te
     for (int i = 0; i < 4; ++i)
         if (q->ne[i] < 1 || v->ne[i] < 1) return 0;
     if (q->ne[0] != kS || v->ne[0] != kS || !fits(q->ne[3], q->ne[2], q->ne[1], v->ne[1])) return 0;
-    return plan(q->ne[3], q->ne[2], q->ne[1], v->ne[1]).total;
+    // the fp32-I/O plan is the larger one: enough whatever the operands' types
+    return plan(q->ne[3], q->ne[2], q->ne[1], v->ne[1], true).total;
 }
 
 extern "C" int tsa_ggml_gated_delta_net(const tsa_tensor* q, const tsa_tensor* k, const tsa_tensor* v,
@@ -146,7 +150,9 @@ extern "C" int tsa_ggml_gated_delta_net(const tsa_tensor* q, const tsa_tensor* k
                                         size_t ws_bytes, void* stream) {
     int rc = check(q, k, v, g, beta, state, out, state_out, scale);
     if (rc) return rc;
-    const Plan p = plan(q->ne[3], q->ne[2], q->ne[1], v->ne[1]);
+    const bool f32 = q->type == TSA_TYPE_F32 || k->type == TSA_TYPE_F32 || v->type == TSA_TYPE_F32 ||
+                     out->type == TSA_TYPE_F32;
+    const Plan p = plan(q->ne[3], q->ne[2], q->ne[1], v->ne[1], f32);
     if (!ws || ws_bytes < p.total) return TSA_ERR_WORKSPACE;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     unsigned char* w = static_cast<unsigned char*>(ws);
@@ -161,9 +167,9 @@ extern "C" int tsa_ggml_gated_delta_net(const tsa_tensor* q, const tsa_tensor* k
                                   dense_view(t.ne, f16 ? 2 : 4), st);
         return dst;
     };
-    const void* qd = operand(*q, p.q, true);
-    const void* kd = operand(*k, p.k, true);
-    const void* vd = operand(*v, p.v, true);
+    const void* qd = operand(*q, p.q, !f32);
+    const void* kd = operand(*k, p.k, !f32);
+    const void* vd = operand(*v, p.v, !f32);
     const float* gd = static_cast<const float*>(operand(*g, p.g, false));
     const float* bd = static_cast<const float*>(operand(*beta, p.beta, false));
     // the state the kernels update in place: state_out itself when it is dense, else scratch
@@ -171,18 +177,18 @@ extern "C" int tsa_ggml_gated_delta_net(const tsa_tensor* q, const tsa_tensor* k
                                   : reinterpret_cast<float*>(w + p.state);
     if (ok() && !(state->data == static_cast<void*>(sd) && dense(*state)))
         e = tsa::copy4d(state->data, 0, view_of(*state), sd, 0, dense_view(state->ne, 4), st);
-    const bool out_direct = dense(*out) && out->type == TSA_TYPE_F16;
+    const bool out_direct = dense(*out) && (out->type == TSA_TYPE_F32) == f32;
     void* od = out_direct ? out->data : static_cast<void*>(w + p.out);
     if (!ok()) return TSA_ERR_LAUNCH;
 
     const int B = (int)p.B, T = (int)p.T, Hk = (int)p.Hk, Hv = (int)p.Hv;
     if (T >= kChunkedMinT)
-        e = tsa::gdn_chunked(qd, kd, vd, gd, bd, sd, od, B, T, Hk, Hv, scale, w + p.chunk, st);
+        e = tsa::gdn_chunked(qd, kd, vd, gd, bd, sd, od, B, T, Hk, Hv, scale, w + p.chunk, f32, st);
     else  // T == 1 takes the decode kernel inside gdn_recurrent
-        e = tsa::gdn_recurrent(qd, kd, vd, gd, bd, sd, od, B, T, Hk, Hv, scale, st);
+        e = tsa::gdn_recurrent(qd, kd, vd, gd, bd, sd, od, B, T, Hk, Hv, scale, f32, st);
     if (ok() && !out_direct)
-        e = tsa::copy4d(od, 1, dense_view(out->ne, 2), out->data, out->type == TSA_TYPE_F16,
-                        view_of(*out), st);
+        e = tsa::copy4d(od, f32 ? 0 : 1, dense_view(out->ne, f32 ? 4 : 2), out->data,
+                        out->type == TSA_TYPE_F16, view_of(*out), st);
     if (ok() && sd != state_out->data)
         e = tsa::copy4d(sd, 0, dense_view(state_out->ne, 4), state_out->data, 0, view_of(*state_out), st);
     return ok() ? TSA_OK : TSA_ERR_LAUNCH;

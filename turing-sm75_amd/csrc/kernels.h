@@ -27,10 +27,11 @@ struct GdnRawGates {
     float eps;
 };
 
-size_t gdn_chunked_ws_bytes(int B, int T, int Hv);
+// f32: q / k / v / out are fp32 (the reference's own I/O; a larger workspace), else fp16.
+size_t gdn_chunked_ws_bytes(int B, int T, int Hv, bool f32 = false);
 hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,
                        const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
-                       float scale, void* ws, hipStream_t stream);
+                       float scale, void* ws, bool f32, hipStream_t stream);
 // The chunked prefill without a caller workspace: the library's fixed device scratch array
 // (gdn_chunked_noalloc_max_bytes() bytes per GPU) stands in for it; no allocation, no side
 // stream.  The caller checks gdn_chunked_ws_bytes(...) against the maximum.
@@ -40,10 +41,12 @@ hipError_t gdn_chunked_noalloc(const void* q, const void* k, const void* v, cons
                                int Hv, float scale, hipStream_t stream);
 // Carry workgroups of the last call on ws that gave up waiting and were redone by the second
 // launch (synchronises `stream`).
-hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, int* count, hipStream_t stream);
+hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, bool f32, int* count,
+                                  hipStream_t stream);
+// f32: q / k / v / out are fp32 (the reference's own I/O), else fp16.
 hipError_t gdn_recurrent(const void* q, const void* k, const void* v, const float* g_log,
                          const float* beta, float* state, void* out, int B, int T, int Hq,
-                         int Hv, float scale, hipStream_t stream);
+                         int Hv, float scale, bool f32, hipStream_t stream);
 hipError_t gdn_chunked_fused(const void* q, const void* k, const void* v, const GdnRawGates& gates,
                              float* state, void* out, int B, int T, int Hq, int Hv, float scale,
                              void* ws, hipStream_t stream);
@@ -67,6 +70,6 @@ hipError_t copy4d(const void* src, int src_f16, const View4& s, void* dst, int d
 
 hipError_t gdn_naive(const void* q, const void* k, const void* v, const float* g_log,
                      const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
-                     int dk, int dv, float scale, hipStream_t stream);
+                     int dk, int dv, float scale, bool f32, hipStream_t stream);
 
 }  // namespace tsa

@@ -1,28 +1,32 @@
 // gdn -- the Gated DeltaNet lab driver, rebuilt over the tsa C-ABI.
 //
-//   gdn [T] [--hv 48] [--hq 16] [--batch B] [--dist lcg|normal] [--mode prefill|decode]
-//       [--steps N] [--seed N] [--iters N]
+//   gdn [T] [--hv 48] [--hq 16] [--batch B] [--dist lcg|normal] [--io f32|f16]
+//       [--mode prefill|decode] [--steps N] [--seed N] [--iters N]
 //
 // Mirrors main() of src/gdn_sm75.cu:1246-1412: T (default 64), shape d = 128, Hq = 16,
-// Hv = 48, scale 1/sqrt(128), the reference's LCG inputs (--dist lcg, :1270-1279; the fp32
-// values are rounded to fp16 for q/k/v, the library's I/O type), state zero, every kernel
-// checked against the naive kernel (max |out - naive| < 0.02, plus the fp32 state within
-// 1e-3 relative), state reset before each checked launch (:1316), 20 timed launches,
-// "ms x48 layers" (:1331).  --dist normal draws q, k ~ N(0,1) with L2-normalised rows,
-// v ~ N(0,1), beta = sigmoid(N(0,1)), g_log = -softplus(N(0,1)).  --mode decode runs
-// --steps single-token steps for --batch sequences from a N(0, 0.02) state.
+// Hv = 48, scale 1/sqrt(128), the reference's LCG inputs (--dist lcg, :1270-1279), state
+// zero, every kernel checked against the naive kernel (max |out - naive| < 0.02, plus the
+// fp32 state within 1e-3 relative), state reset before each checked launch (:1316), 20 timed
+// launches, "ms x48 layers" (:1331).  --io f32 (the default with the LCG inputs) runs q / k /
+// v / out in fp32 through the *_f32 entry points, the reference's own precision (:57-64);
+// --io f16 (the default with --dist normal) rounds them to fp16, the library's I/O type.
+// --dist normal draws q, k ~ N(0,1) with L2-normalised rows, v ~ N(0,1), beta =
+// sigmoid(N(0,1)), g_log = -softplus(N(0,1)).  --mode decode runs --steps single-token
+// steps for --batch sequences from a N(0, 0.02) state.
 #include <algorithm>
 
 #include "driver_util.h"
 
 namespace {
 
+template <typename E>
 struct Inputs {
-    std::vector<f16> q, k, v;
+    std::vector<E> q, k, v;
     std::vector<float> g, b, st;
 };
 
-void gen(Inputs& in, const std::string& dist, int B, int T, int Hq, int Hv, int d, unsigned seed,
+template <typename E>
+void gen(Inputs<E>& in, const std::string& dist, int B, int T, int Hq, int Hv, int d, unsigned seed,
          bool state_noise) {
     const size_t nqk = (size_t)B * T * Hq * d, nv = (size_t)B * T * Hv * d, ng = (size_t)B * T * Hv;
     in.q.resize(nqk);
@@ -37,16 +41,16 @@ void gen(Inputs& in, const std::string& dist, int B, int T, int Hq, int Hv, int 
             s = s * 1664525u + 1013904223u;
             return ((float)(s >> 8) / 16777216.f) - 0.5f;
         };
-        for (auto& x : in.q) x = (f16)(rnd() * 0.2f);
-        for (auto& x : in.k) x = (f16)(rnd() * 0.2f);
-        for (auto& x : in.v) x = (f16)(rnd() * 0.2f);
+        for (auto& x : in.q) x = (E)(rnd() * 0.2f);
+        for (auto& x : in.k) x = (E)(rnd() * 0.2f);
+        for (auto& x : in.v) x = (E)(rnd() * 0.2f);
         for (auto& x : in.g) x = -0.2f + rnd() * 0.05f;
         for (auto& x : in.b) x = 0.4f + (rnd() + 0.5f) * 0.4f;
     } else {
         std::mt19937 rng(seed);
         std::normal_distribution<float> n01(0.f, 1.f);
         std::vector<float> row(d);
-        for (std::vector<f16>* t : {&in.q, &in.k}) {
+        for (std::vector<E>* t : {&in.q, &in.k}) {
             for (size_t r = 0; r < t->size() / d; ++r) {
                 double ss = 0;
                 for (int i = 0; i < d; ++i) {
@@ -54,10 +58,10 @@ void gen(Inputs& in, const std::string& dist, int B, int T, int Hq, int Hv, int 
                     ss += (double)row[i] * row[i];
                 }
                 const float inv = (float)(1.0 / std::sqrt(ss));
-                for (int i = 0; i < d; ++i) (*t)[r * d + i] = (f16)(row[i] * inv);
+                for (int i = 0; i < d; ++i) (*t)[r * d + i] = (E)(row[i] * inv);
             }
         }
-        for (auto& x : in.v) x = (f16)n01(rng);
+        for (auto& x : in.v) x = (E)n01(rng);
         for (auto& x : in.b) x = 1.f / (1.f + std::exp(-n01(rng)));
         for (auto& x : in.g) {
             const float z = n01(rng);
@@ -71,7 +75,8 @@ void gen(Inputs& in, const std::string& dist, int B, int T, int Hq, int Hv, int 
     }
 }
 
-float max_abs(const std::vector<f16>& a, const std::vector<f16>& b) {
+template <typename E>
+float max_abs(const std::vector<E>& a, const std::vector<E>& b) {
     float m = 0.f;
     for (size_t i = 0; i < a.size(); ++i) {
         const float d = std::fabs((float)a[i] - (float)b[i]);
@@ -92,37 +97,52 @@ float rel_state(const std::vector<float>& a, const std::vector<float>& ref) {
 
 }  // namespace
 
-int main(int argc, char** argv) {
-    Opts opt(argc, argv);
-    if (opt.bad || opt.pos.size() > 1 ||
-        !opt.known({"hv", "hq", "batch", "dist", "mode", "steps", "seed", "iters"})) {
-        std::fprintf(stderr, "usage: %s [T] [--hv N] [--hq N] [--batch B] [--dist lcg|normal] [--mode prefill|decode] [--steps N] [--seed N] [--iters N]\n", argv[0]);
-        return 2;
+// The entry points for each I/O type: fp16 (the library's) or fp32 (the *_f32 forms).
+template <typename E> struct Api;
+template <> struct Api<f16> {
+    static constexpr auto ws_bytes = tsa_gdn_chunked_workspace_bytes;
+    static int chunked(const f16* q, const f16* k, const f16* v, const float* g, const float* b, float* s,
+                       f16* o, int B, int T, int Hq, int Hv, int dk, int dv, int c, float sc, void* ws,
+                       size_t wsb, void* st) {
+        return tsa_gdn_chunked_fwd(q, k, v, g, b, s, o, B, T, Hq, Hv, dk, dv, c, sc, ws, wsb, st);
     }
-    const std::string mode = opt.get("mode", "prefill");
-    const std::string dist = opt.get("dist", mode == "decode" ? "normal" : "lcg");
-    int T = opt.pos.empty() ? 64 : std::atoi(opt.pos[0].c_str());
-    const int Hv = std::atoi(opt.get("hv", "48").c_str());
-    const int Hq = std::atoi(opt.get("hq", "16").c_str());
-    const int B = std::atoi(opt.get("batch", mode == "decode" ? "16" : "1").c_str());
-    const int steps = std::atoi(opt.get("steps", "64").c_str());
-    const unsigned seed = (unsigned)std::strtoul(opt.get("seed", "1").c_str(), nullptr, 10);
-    const int iters = std::atoi(opt.get("iters", "20").c_str());
-    const int d = 128;
-    if (T < 1 || Hv < 1 || Hq < 1 || B < 1 || steps < 1 || iters < 1 ||
-        (mode != "prefill" && mode != "decode") || (dist != "lcg" && dist != "normal")) {
-        std::fprintf(stderr, "usage: %s [T] ... (T, heads, batch, steps >= 1)\n", argv[0]);
-        return 2;
+    static int recurrent(const f16* q, const f16* k, const f16* v, const float* g, const float* b, float* s,
+                         f16* o, int B, int T, int Hq, int Hv, int dk, int dv, float sc, void* st) {
+        return tsa_gdn_recurrent_fwd(q, k, v, g, b, s, o, B, T, Hq, Hv, dk, dv, sc, st);
     }
-    const float scale = 1.f / std::sqrt((float)d);
-    print_gpu();
-    if (mode == "decode") T = steps;
-    std::printf("GDN shape       : d=%d  Hq=%d  Hv=%d  B=%d  T=%d  C=64  mode=%s  dist=%s\n", d, Hq,
-                Hv, B, T, mode.c_str(), dist.c_str());
+    static int naive(const f16* q, const f16* k, const f16* v, const float* g, const float* b, float* s,
+                     f16* o, int B, int T, int Hq, int Hv, int dk, int dv, float sc, void* st) {
+        return tsa_gdn_naive(q, k, v, g, b, s, o, B, T, Hq, Hv, dk, dv, sc, st);
+    }
+    static int decode(const f16* q, const f16* k, const f16* v, const float* g, const float* b, float* s,
+                      f16* o, int B, int Hq, int Hv, int dk, int dv, float sc, void* st) {
+        return tsa_gdn_decode_step(q, k, v, g, b, s, o, B, Hq, Hv, dk, dv, sc, st);
+    }
+};
+template <> struct Api<float> {
+    static constexpr auto ws_bytes = tsa_gdn_chunked_workspace_bytes_f32;
+    static constexpr auto chunked = tsa_gdn_chunked_fwd_f32;
+    static constexpr auto recurrent = tsa_gdn_recurrent_fwd_f32;
+    static constexpr auto naive = tsa_gdn_naive_f32;
+    static constexpr auto decode = tsa_gdn_decode_step_f32;
+};
 
-    Inputs in;
-    gen(in, dist, B, T, Hq, Hv, d, seed, mode == "decode");
-    DevBuf<f16> q(in.q.size()), k(in.k.size()), v(in.v.size()), o_ref(in.v.size()), o(in.v.size());
+struct Shape {
+    std::string mode, dist;
+    int T, Hv, Hq, B;
+    unsigned seed;
+    int iters, d;
+    float scale;
+};
+
+template <typename E>
+int run(const Shape& sh) {
+    const std::string &mode = sh.mode, &dist = sh.dist;
+    const int T = sh.T, Hv = sh.Hv, Hq = sh.Hq, B = sh.B, iters = sh.iters, d = sh.d;
+    const float scale = sh.scale;
+    Inputs<E> in;
+    gen(in, dist, B, T, Hq, Hv, d, sh.seed, mode == "decode");
+    DevBuf<E> q(in.q.size()), k(in.k.size()), v(in.v.size()), o_ref(in.v.size()), o(in.v.size());
     DevBuf<float> g(in.g.size()), b(in.b.size()), st_ref(in.st.size()), st(in.st.size());
     q.upload(in.q);
     k.upload(in.k);
@@ -130,9 +150,9 @@ int main(int argc, char** argv) {
     g.upload(in.g);
     b.upload(in.b);
     st_ref.upload(in.st);
-    DRV_TSA(tsa_gdn_naive(q.d, k.d, v.d, g.d, b.d, st_ref.d, o_ref.d, B, T, Hq, Hv, d, d, scale, nullptr));
+    DRV_TSA(Api<E>::naive(q.d, k.d, v.d, g.d, b.d, st_ref.d, o_ref.d, B, T, Hq, Hv, d, d, scale, nullptr));
     DRV_HIP(hipDeviceSynchronize());
-    std::vector<f16> ho_ref, ho;
+    std::vector<E> ho_ref, ho;
     std::vector<float> hs_ref, hs;
     o_ref.download(ho_ref);
     st_ref.download(hs_ref);
@@ -151,13 +171,13 @@ int main(int argc, char** argv) {
     const double state_bytes = 2.0 * B * Hv * d * d * 4;  // read + write per launch
 
     if (mode == "prefill") {
-        const size_t wsb = tsa_gdn_chunked_workspace_bytes(B, T, Hq, Hv, d, d, 64);
+        const size_t wsb = Api<E>::ws_bytes(B, T, Hq, Hv, d, d, 64);
         DevBuf<unsigned char> ws(wsb);
         auto chunked = [&] {
-            DRV_TSA(tsa_gdn_chunked_fwd(q.d, k.d, v.d, g.d, b.d, st.d, o.d, B, T, Hq, Hv, d, d, 64, scale, ws.d, wsb, nullptr));
+            DRV_TSA(Api<E>::chunked(q.d, k.d, v.d, g.d, b.d, st.d, o.d, B, T, Hq, Hv, d, d, 64, scale, ws.d, wsb, nullptr));
         };
         auto recurrent = [&] {
-            DRV_TSA(tsa_gdn_recurrent_fwd(q.d, k.d, v.d, g.d, b.d, st.d, o.d, B, T, Hq, Hv, d, d, scale, nullptr));
+            DRV_TSA(Api<E>::recurrent(q.d, k.d, v.d, g.d, b.d, st.d, o.d, B, T, Hq, Hv, d, d, scale, nullptr));
         };
         const double tokens = (double)B * T;
         for (auto kv : {std::make_pair("chunked", 0), std::make_pair("recurrent", 1)}) {
@@ -172,7 +192,7 @@ int main(int argc, char** argv) {
         // T = steps single-token launches; inputs of step t are token t of each sequence,
         // so the step-major decode layout [B][Hq][d] is a strided view: copy per step.
         const size_t sq = (size_t)B * Hq * d, sv = (size_t)B * Hv * d, sg = (size_t)B * Hv;
-        std::vector<f16> dq(sq * T), dk(sq * T), dvv(sv * T);
+        std::vector<E> dq(sq * T), dk(sq * T), dvv(sv * T);
         std::vector<float> dg(sg * T), db(sg * T);
         for (int t = 0; t < T; ++t)
             for (int bb = 0; bb < B; ++bb) {
@@ -182,7 +202,7 @@ int main(int argc, char** argv) {
                 std::copy_n(&in.g[((size_t)bb * T + t) * Hv], Hv, &dg[t * sg + (size_t)bb * Hv]);
                 std::copy_n(&in.b[((size_t)bb * T + t) * Hv], Hv, &db[t * sg + (size_t)bb * Hv]);
             }
-        DevBuf<f16> Dq(dq.size()), Dk(dk.size()), Dv(dvv.size()), Do(dvv.size());
+        DevBuf<E> Dq(dq.size()), Dk(dk.size()), Dv(dvv.size()), Do(dvv.size());
         DevBuf<float> Dg(dg.size()), Db(db.size());
         Dq.upload(dq);
         Dk.upload(dk);
@@ -191,20 +211,20 @@ int main(int argc, char** argv) {
         Db.upload(db);
         auto run_steps = [&] {
             for (int t = 0; t < T; ++t)
-                DRV_TSA(tsa_gdn_decode_step(Dq.d + t * sq, Dk.d + t * sq, Dv.d + t * sv, Dg.d + t * sg,
-                                            Db.d + t * sg, st.d, Do.d + t * sv, B, Hq, Hv, d, d, scale, nullptr));
+                DRV_TSA(Api<E>::decode(Dq.d + t * sq, Dk.d + t * sq, Dv.d + t * sv, Dg.d + t * sg,
+                                       Db.d + t * sg, st.d, Do.d + t * sv, B, Hq, Hv, d, d, scale, nullptr));
         };
         st.upload(in.st);
         run_steps();
         DRV_HIP(hipDeviceSynchronize());
         // reorder step-major outputs back to [B][T][Hv][d] for the comparison
-        std::vector<f16> so;
+        std::vector<E> so;
         Do.download(so);
-        std::vector<f16> ho2(so.size());
+        std::vector<E> ho2(so.size());
         for (int t = 0; t < T; ++t)
             for (int bb = 0; bb < B; ++bb)
                 std::copy_n(&so[t * sv + (size_t)bb * Hv * d], Hv * d, &ho2[((size_t)bb * T + t) * Hv * d]);
-        DRV_HIP(hipMemcpy(o.d, ho2.data(), ho2.size() * sizeof(f16), hipMemcpyHostToDevice));
+        DRV_HIP(hipMemcpy(o.d, ho2.data(), ho2.size() * sizeof(E), hipMemcpyHostToDevice));
         check("decode");
         const float ms = time_ms(run_steps, std::max(1, iters / 4)) / T;
         std::printf("%-16s: %8.5f ms/step   %.1f GB/s state traffic   %.3e tok/s\n", "decode", ms,
@@ -213,3 +233,37 @@ int main(int argc, char** argv) {
     const bool ok = worst_out < 2e-2f && worst_state < 1e-3f;
     return ok ? 0 : 1;
 }
+
+int main(int argc, char** argv) {
+    Opts opt(argc, argv);
+    if (opt.bad || opt.pos.size() > 1 ||
+        !opt.known({"hv", "hq", "batch", "dist", "io", "mode", "steps", "seed", "iters"})) {
+        std::fprintf(stderr, "usage: %s [T] [--hv N] [--hq N] [--batch B] [--dist lcg|normal] [--io f32|f16] [--mode prefill|decode] [--steps N] [--seed N] [--iters N]\n", argv[0]);
+        return 2;
+    }
+    const std::string mode = opt.get("mode", "prefill");
+    const std::string dist = opt.get("dist", mode == "decode" ? "normal" : "lcg");
+    const std::string io = opt.get("io", dist == "lcg" ? "f32" : "f16");
+    int T = opt.pos.empty() ? 64 : std::atoi(opt.pos[0].c_str());
+    const int Hv = std::atoi(opt.get("hv", "48").c_str());
+    const int Hq = std::atoi(opt.get("hq", "16").c_str());
+    const int B = std::atoi(opt.get("batch", mode == "decode" ? "16" : "1").c_str());
+    const int steps = std::atoi(opt.get("steps", "64").c_str());
+    const unsigned seed = (unsigned)std::strtoul(opt.get("seed", "1").c_str(), nullptr, 10);
+    const int iters = std::atoi(opt.get("iters", "20").c_str());
+    const int d = 128;
+    if (T < 1 || Hv < 1 || Hq < 1 || B < 1 || steps < 1 || iters < 1 ||
+        (mode != "prefill" && mode != "decode") || (dist != "lcg" && dist != "normal") ||
+        (io != "f32" && io != "f16")) {
+        std::fprintf(stderr, "usage: %s [T] ... (T, heads, batch, steps >= 1)\n", argv[0]);
+        return 2;
+    }
+    const float scale = 1.f / std::sqrt((float)d);
+    print_gpu();
+    if (mode == "decode") T = steps;
+    std::printf("GDN shape       : d=%d  Hq=%d  Hv=%d  B=%d  T=%d  C=64  mode=%s  dist=%s  io=%s\n", d,
+                Hq, Hv, B, T, mode.c_str(), dist.c_str(), io.c_str());
+    const Shape sh{mode, dist, T, Hv, Hq, B, seed, iters, d, scale};
+    return io == "f32" ? run<float>(sh) : run<f16>(sh);
+}
+

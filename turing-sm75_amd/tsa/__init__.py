@@ -57,7 +57,12 @@ _SIGNATURES = {
     "tsa_gdn_chunked_workspace_bytes": (_sz, [_i] * 7),
     "tsa_gdn_chunked_fwd": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp, _sz, _vp]),
     "tsa_gdn_chunked_fwd_noalloc": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp]),
-    "tsa_gdn_chunked_redo_count": (_i, [_vp, _sz] + [_i] * 7 + [ctypes.POINTER(ctypes.c_int), _vp]),
+    "tsa_gdn_chunked_redo_count": (_i, [_vp, _sz] + [_i] * 8 + [ctypes.POINTER(ctypes.c_int), _vp]),
+    "tsa_gdn_chunked_workspace_bytes_f32": (_sz, [_i] * 7),
+    "tsa_gdn_chunked_fwd_f32": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp, _sz, _vp]),
+    "tsa_gdn_recurrent_fwd_f32": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
+    "tsa_gdn_decode_step_f32": (_i, [_vp] * 7 + [_i] * 5 + [_f, _vp]),
+    "tsa_gdn_naive_f32": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
     "tsa_gdn_recurrent_fwd": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
     "tsa_gdn_decode_step": (_i, [_vp] * 7 + [_i] * 5 + [_f, _vp]),
     "tsa_gdn_naive": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
@@ -216,10 +221,13 @@ def attn_gqa_fwd(q, k, v, gate=None, out=None, scale=None, causal=True, stream=N
 # Gated DeltaNet
 # ---------------------------------------------------------------------------------------
 def _gdn_shapes(q, k, v, g_log, beta, state, batched_t: bool):
+    """Shapes of a GDN call; q, k, v are all fp16 (the library's I/O type) or all fp32 (the
+    *_f32 entry points, the reference's own I/O)."""
     import torch
     nd = 4 if batched_t else 3
+    io = q.dtype if isinstance(q, torch.Tensor) and q.dtype in (torch.float16, torch.float32) else torch.float16
     for name, t in (("q", q), ("k", k), ("v", v)):
-        _need(t, torch.float16, nd, name)
+        _need(t, io, nd, name)
     _need(g_log, torch.float32, nd - 1, "g_log")
     _need(beta, torch.float32, nd - 1, "beta")
     _need(state, torch.float32, 4, "state")
@@ -241,59 +249,68 @@ def _gdn_shapes(q, k, v, g_log, beta, state, batched_t: bool):
     return B, T, Hq, Hv, dk, dv
 
 
-def gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk=128, dv=128, chunk=64) -> int:
-    return int(load().tsa_gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk))
+def gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk=128, dv=128, chunk=64, f32=False) -> int:
+    fn = load().tsa_gdn_chunked_workspace_bytes_f32 if f32 else load().tsa_gdn_chunked_workspace_bytes
+    return int(fn(B, T, Hq, Hv, dk, dv, chunk))
 
 
 def gdn_chunked_fwd(q, k, v, g_log, beta, state, out=None, scale=None, chunk=64, ws=None,
                     stream=None):
-    """Chunked prefill; state [B, Hv, dv, dk] is updated in place; returns out."""
+    """Chunked prefill; state [B, Hv, dv, dk] is updated in place; returns out.  fp32 q/k/v
+    select tsa_gdn_chunked_fwd_f32 (fp32 out)."""
     import torch
     B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, True)
     out = _out(out, v)
     if scale is None:
         scale = 1.0 / math.sqrt(dk)
-    need = gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk)
+    f32 = q.dtype == torch.float32
+    need = gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk, f32=f32)
     if ws is None:
         ws = _scratch(need, q.device, stream)
-    _check(load().tsa_gdn_chunked_fwd(
+    fn = load().tsa_gdn_chunked_fwd_f32 if f32 else load().tsa_gdn_chunked_fwd
+    _check(fn(
         _ptr(q), _ptr(k), _ptr(v), _ptr(g_log), _ptr(beta), _ptr(state), _ptr(out),
         B, T, Hq, Hv, dk, dv, chunk, float(scale), _ptr(ws), ws.numel() * ws.element_size(),
         _stream(stream)))
     return out
 
 
-def gdn_chunked_redo_count(ws, B, T, Hq, Hv, dk=128, dv=128, chunk=64, stream=None) -> int:
+def gdn_chunked_redo_count(ws, B, T, Hq, Hv, dk=128, dv=128, chunk=64, f32=False, stream=None) -> int:
     """Carry workgroups of the last chunked call on ws that were redone after a timed-out wait
     (0 when prep and carry ran side by side); synchronises the stream."""
     c = ctypes.c_int(-1)
     _check(load().tsa_gdn_chunked_redo_count(_ptr(ws), ws.numel() * ws.element_size(), B, T, Hq,
-                                             Hv, dk, dv, chunk, ctypes.byref(c), _stream(stream)))
+                                             Hv, dk, dv, chunk, int(bool(f32)), ctypes.byref(c),
+                                             _stream(stream)))
     return c.value
 
 
 def gdn_recurrent_fwd(q, k, v, g_log, beta, state, out=None, scale=None, stream=None,
                       naive=False):
-    """Token-serial recurrence over T tokens (or the naive check kernel); state in place."""
+    """Token-serial recurrence over T tokens (or the naive check kernel); state in place.
+    fp32 q/k/v select the *_f32 entry points."""
     import torch
     B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, True)
     out = _out(out, v)
     if scale is None:
         scale = 1.0 / math.sqrt(dk)
-    fn = load().tsa_gdn_naive if naive else load().tsa_gdn_recurrent_fwd
+    sfx = "_f32" if q.dtype == torch.float32 else ""
+    fn = getattr(load(), ("tsa_gdn_naive" if naive else "tsa_gdn_recurrent_fwd") + sfx)
     _check(fn(_ptr(q), _ptr(k), _ptr(v), _ptr(g_log), _ptr(beta), _ptr(state), _ptr(out),
               B, T, Hq, Hv, dk, dv, float(scale), _stream(stream)))
     return out
 
 
 def gdn_decode_step(q, k, v, g_log, beta, state, out=None, scale=None, stream=None):
-    """One token per sequence: q/k [B, Hq, dk], v [B, Hv, dv]; state in place."""
+    """One token per sequence: q/k [B, Hq, dk], v [B, Hv, dv]; state in place (fp16 or fp32
+    q/k/v/out)."""
     import torch
     B, _, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, False)
     out = _out(out, v)
     if scale is None:
         scale = 1.0 / math.sqrt(dk)
-    _check(load().tsa_gdn_decode_step(
+    fn = load().tsa_gdn_decode_step_f32 if q.dtype == torch.float32 else load().tsa_gdn_decode_step
+    _check(fn(
         _ptr(q), _ptr(k), _ptr(v), _ptr(g_log), _ptr(beta), _ptr(state), _ptr(out),
         B, Hq, Hv, dk, dv, float(scale), _stream(stream)))
     return out
@@ -320,8 +337,10 @@ def _gates(a, b, dt_bias, A, lead, Hv):
 
 def gdn_chunked_fused_fwd(q, k, v, a, b, dt_bias, A, state, out=None, scale=None, eps=1e-6,
                           chunk=64, ws=None, stream=None):
-    """Chunked prefill from raw q, k [B,T,Hq,dk] and raw gate projections a, b [B,T,Hv]."""
+    """Chunked prefill from raw q, k [B,T,Hq,dk] and raw gate projections a, b [B,T,Hv]
+    (fp16 q / k / v / out)."""
     import torch
+    _need(q, torch.float16, 4, "q")
     B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, a, b, state, True)
     _gates(a, b, dt_bias, A, (B, T), Hv)
     out = _out(out, v)
@@ -339,8 +358,10 @@ def gdn_chunked_fused_fwd(q, k, v, a, b, dt_bias, A, state, out=None, scale=None
 
 def gdn_decode_fused_step(q, k, v, a, b, dt_bias, A, state, out=None, scale=None, eps=1e-6,
                           stream=None):
-    """One decode step from raw q, k [B,Hq,dk] and raw gate projections a, b [B,Hv]."""
+    """One decode step from raw q, k [B,Hq,dk] and raw gate projections a, b [B,Hv] (fp16
+    q / k / v / out)."""
     import torch
+    _need(q, torch.float16, 3, "q")
     B, _, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, a, b, state, False)
     _gates(a, b, dt_bias, A, (B,), Hv)
     out = _out(out, v)
