@@ -67,14 +67,16 @@ __device__ __forceinline__ int chunk_pos(int r, int c) {
 }
 
 // Map the linear workgroup id to (bh, query tile).  Workgroups are dispatched round
-// robin over the 8 XCDs; when BH is a multiple of 8, head bh runs on XCD bh % 8.  Causal
-// runs issue the longest (highest) query tiles first.
+// robin over the 8 XCDs; when BH is a multiple of 8, XCD x runs the contiguous heads
+// x * BH/8 .. (x + 1) * BH/8 - 1, so the query heads of one K/V group (adjacent head
+// numbers) share an XCD and read their K/V tiles through the same L2.  Causal runs issue
+// the longest (highest) query tiles first.
 __device__ __forceinline__ void map_block(int bid, int BH, int n_qt, bool causal, int& bh,
                                           int& qt) {
     int rank;
     if ((BH & 7) == 0) {
         const int xcd = bid & 7, slot = bid >> 3, hpx = BH >> 3;
-        bh = (slot % hpx) * 8 + xcd;
+        bh = xcd * hpx + slot % hpx;
         rank = slot / hpx;
     } else {
         bh = bid % BH;
