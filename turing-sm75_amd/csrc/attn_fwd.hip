@@ -3,8 +3,9 @@
 // Same recurrence as flash_attn_sm75_wmma (src/attn_sm75.cu:239-375): stream K/V tiles,
 // keep running (m, l, O) per query row, O = O*alpha + P V, finally O / l.  The tiling is
 // CDNA4-shaped instead of a 16x16 warp tile:
-//   * a workgroup is 4 waves and owns 128 query rows (32 per wave); K/V tiles of 64 keys
-//     are double-buffered in LDS (64 KiB at D = 128) so two workgroups share a CU, and
+//   * a workgroup is 4 waves and owns 128 query rows (32 per wave, 8 waves at D = 256);
+//     K/V tiles of 64 keys are double-buffered in LDS (64 KiB at D = 128) so two
+//     workgroups share a CU, and
 //     copied there by LDS-DMA (global_load_lds_dwordx4, per-lane offsets computed once,
 //     the bank swizzle applied on the source side), so no register stages them;
 //   * each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_f16 (A = K rows from LDS,
@@ -24,8 +25,11 @@
 //   * grouped-query attention and the output gate of gated attention (the D = 256 layers
 //     of the reference's target model, docs/qwen38-27b.md:13): query head h reads K/V
 //     head h / (Hq / Hkv), and O is multiplied by sigmoid(gate) when a gate is given.
-//     At D = 256 a wave's 32 query rows need ~280 registers (Q operands 64, O^T 128), so
-//     the workgroup runs one wave per SIMD with the 128 KiB of K/V tiles to itself.
+//     At D = 256 a workgroup is 8 waves (256 query rows) sharing one 128 KiB set of K/V
+//     tiles, two waves per SIMD at 256 registers each (Q operands 64, O^T 128): LDS
+//     addresses are one XOR with an immediate per read and the tile copies need one offset
+//     register, so the rest fits.
+#include <climits>
 #include <type_traits>
 
 #include "common.h"
@@ -34,8 +38,6 @@
 namespace tsa {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kQRows = 128;  // query rows per workgroup
 constexpr int kKRows = 64;   // keys per LDS tile
 
 // 16-byte chunk swizzle of an LDS tile row: chunk c of row r lives at c ^ swz<D>(r).
@@ -87,15 +89,27 @@ __device__ __forceinline__ void map_block(int bid, int BH, int n_qt, bool causal
 
 typedef __attribute__((address_space(3))) void* lds_void_t;
 
+// LDS reads at a byte address held as an integer (so that address arithmetic can be an
+// XOR with an immediate plus an offset folded into the instruction).
+__device__ __forceinline__ half8_t lds_read_b128(unsigned addr) {
+    typedef __attribute__((address_space(3))) const half8_t* p_t;
+    return *(p_t)(addr);
+}
+__device__ __forceinline__ half4_t lds_read_tr16_at(unsigned addr) {
+    typedef __attribute__((address_space(3))) fp16x4_t* p_t;
+    return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((p_t)(addr)));
+}
+
 // K/V tile copy plan.  One LDS-DMA instruction moves 1 KiB (lane l: 16 bytes to M0 + 16*l);
-// a tile of 64 rows x D halfs is kDmaTile instructions, K then V, and wave w issues
-// instructions w + 4j.  LDS chunk position p of row r holds source chunk p ^ swz(r), so
+// a tile of 64 rows x D halfs is kTile instructions, K then V, and wave w of kW issues
+// instructions w + kW j.  LDS chunk position p of row r holds source chunk p ^ swz(r), so
 // the tile lands in the same swizzled layout the operand reads expect.
-template <int D>
+template <int D, int kW = 4>
 struct Dma {
     static constexpr int kTile = kKRows * D * 2 / 1024;  // instructions per K (or V) tile
-    static constexpr int kPerWave = 2 * kTile / 4;
+    static constexpr int kPerWave = 2 * kTile / kW;      // for kW waves per workgroup
     static constexpr int kChunks = D / 8;
+    static_assert(kTile % kW == 0, "each wave copies whole groups of K and V blocks");
 };
 template <int D>
 __device__ __forceinline__ unsigned dma_off(int blk, int lane, int lastrow) {
@@ -114,29 +128,42 @@ __device__ __forceinline__ void dma_issue(const void* base, unsigned off, unsign
 }
 // This wave's share of the copies of K/V rows k0..k0+63 into the buffer at lds_buf, in
 // two halves (kPart 0: j < kPerWave/2, kPart 1: the rest) so each can be issued between
-// MFMAs.
-template <int D, int kPart>
-__device__ __forceinline__ void copy_tile(const unsigned (&off)[Dma<D>::kPerWave], int wave,
-                                          const half_t* Kh, const half_t* Vh, int k0, int S,
-                                          unsigned lds_buf) {
-    const int lane = threadIdx.x & 63;
+// MFMAs.  off0 = dma_off(wave, lane, 63).  Wave w copies blocks w + kW j (K for
+// kW j < kTile, V after).  A block is 1 KiB of whole rows and the swizzle reads row bits
+// 0-3; when all of a wave's blocks see the same row % 16 pattern -- always at D <= 128
+// (blk = w mod 4 fixes it), at D = 256 (two rows per block) when kW is a multiple of 8
+// (blk = w mod 8) -- block blk of a full tile sits at off0 + 1024 (blk - w): one register
+// for all copies.
+template <int D, int kPart, int kW>
+__device__ __forceinline__ void copy_tile(unsigned off0, int wave, const half_t* Kh, const half_t* Vh,
+                                          int k0, int S, unsigned lds_buf) {
+    static_assert(D <= 128 || kW % 8 == 0, "a wave's copy blocks must share one swizzle pattern");
     const half_t* kb = Kh + (size_t)k0 * D;
     const half_t* vb = Vh + (size_t)k0 * D;
     const int lastrow = S - 1 - k0;
     auto issue_all = [&](auto Ragged) {  // a ragged last tile clamps its rows to S - 1
 #pragma unroll
-        for (int j = kPart * Dma<D>::kPerWave / 2; j < (kPart + 1) * Dma<D>::kPerWave / 2; ++j) {
-            const int n = wave + 4 * j;  // wave is uniform; n < 2 * kTile
-            const bool isv = n >= Dma<D>::kTile;
-            const int blk = isv ? n - Dma<D>::kTile : n;
-            const unsigned o = decltype(Ragged)::value ? dma_off<D>(blk, lane, lastrow) : off[j];
+        for (int j = kPart * Dma<D, kW>::kPerWave / 2; j < (kPart + 1) * Dma<D, kW>::kPerWave / 2; ++j) {
+            constexpr int kT = Dma<D>::kTile;  // a multiple of kW, and wave < kW
+            const bool isv = kW * j >= kT;
+            const int dblk = kW * j - (isv ? kT : 0);  // blk - wave
+            unsigned o;
+            if constexpr (!decltype(Ragged)::value) {
+                o = off0 + 1024u * (unsigned)dblk;
+            } else {  // the same offset with its row clamped to S - 1
+                constexpr unsigned kRowB = 2 * D, kRows = 1024 / kRowB;
+                // the empty asm keeps this arithmetic inside the ragged branch (hoisted, its
+                // values take registers for the whole loop)
+                unsigned o0 = off0;
+                asm volatile("" : "+v"(o0));
+                const int row = (int)(o0 / kRowB) + (int)kRows * dblk;
+                o = (unsigned)min(row, lastrow) * kRowB + o0 % kRowB;
+            }
             dma_issue(isv ? (const void*)vb : (const void*)kb, o,
-                      lds_buf + (unsigned)(isv ? kKRows * D * 2 : 0) + 1024u * blk);
+                      lds_buf + (unsigned)(isv ? kKRows * D * 2 : 0) + 1024u * (unsigned)(wave + dblk));
         }
     };
-    // At D = 256 every register counts (one wave per SIMD, the PV loop waits on each V read
-    // when none is free to read ahead): there the offsets are recomputed per copy.
-    if (lastrow >= kKRows - 1 && D <= 128)
+    if (lastrow >= kKRows - 1)
         issue_all(std::false_type{});
     else
         issue_all(std::true_type{});
@@ -146,14 +173,18 @@ __device__ __forceinline__ void dma_wait_barrier() {
     lds_barrier();
 }
 
-template <int D, bool kCausal>
-__global__ void __launch_bounds__(kThreads, D == 256 ? 1 : 2)
+// kW waves per workgroup, 32 query rows each: kW = 4 at D <= 128 (two workgroups per CU,
+// two waves per SIMD), kW = 8 at D = 256 (one workgroup per CU with the 128 KiB of K/V
+// tiles, two waves per SIMD sharing them).
+template <int D, bool kCausal, int kW>
+__global__ void __launch_bounds__(64 * kW, 2)
 attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                 const half_t* __restrict__ V, const half_t* __restrict__ gate,
                 half_t* __restrict__ O, int S, int BH, int n_qt, int Hq, int group,
                 float c2 /* scale * log2(e) */) {
     using C = Cfg<D>;
-    extern __shared__ __align__(16) half_t lds[];
+    // static and 1 KiB aligned: the XOR address forms below need the buffer's low 10 bits zero
+    __shared__ __align__(1024) half_t lds[C::kLdsBytes / 2];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -162,7 +193,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     map_block(blockIdx.x, BH, n_qt, kCausal, bh, qt);
     const size_t head = (size_t)bh * S * D;  // Q, O, gate: query head bh = b * Hq + h
     const size_t kvhead = (size_t)((bh / Hq) * (Hq / group) + (bh % Hq) / group) * S * D;
-    const int q0 = qt * kQRows;
+    const int q0 = qt * (32 * kW);
     const int qw0 = q0 + 32 * wave;
     const int my_q = qw0 + (lane & 31);
 
@@ -177,7 +208,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
             qf[kk] = half8_t{};
     }
 
-    const int kv_end = kCausal ? min(S, q0 + kQRows) : S;
+    const int kv_end = kCausal ? min(S, q0 + 32 * kW) : S;
     const int n_tiles = (kv_end + kKRows - 1) / kKRows;
     const int wave_kv_end = kCausal ? min(S, qw0 + 32) : S;
 
@@ -196,28 +227,28 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const int vchunk = 2 * (g16 & 1) + (vm >> 1);
     const int vsub = 4 * (vm & 1);
 
-    unsigned off[Dma<D>::kPerWave];
-#pragma unroll
-    for (int j = 0; j < Dma<D>::kPerWave; ++j) {
-        const int n = wave + 4 * j;
-        off[j] = D <= 128 ? dma_off<D>(n >= Dma<D>::kTile ? n - Dma<D>::kTile : n, lane, kKRows - 1) : 0u;
-    }
+    const unsigned off = dma_off<D>(wave, lane, kKRows - 1);
     const unsigned lds0 = (unsigned)(uintptr_t)(lds_void_t)(void*)lds;
     const unsigned buf_bytes = 2 * C::kTile * 2;
-    copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, 0, S, lds0);
-    copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, 0, S, lds0);
+    constexpr unsigned kRowB = 2 * D;  // bytes per K/V row in LDS
+    // LDS operand addresses as byte offsets in buffer 0.  A row is 16 * (D / 8) bytes and
+    // starts at a multiple of that, so the chunk field (bits 4.. within the row) can be
+    // XORed without touching the row bits.  K operand of k-step kk (row krow, chunk
+    // (2 kk + hi) ^ swz(krow)): ka ^ (32 kk), since 2 kk + hi = 2 kk ^ hi and swz < 16.
+    // V^T operand of key step ks, column block db, half e (rows 16 ks + 4 hi + vj + 8 e,
+    // chunk (4 db + vchunk) ^ swz(row), element vsub): swz(row) reads row bits 0-3, which
+    // 16 ks leaves alone, so the address is (va[e] ^ 64 db) + 32 D ks.
+    unsigned ka = lds0 + krow * kRowB + 16u * (unsigned)(hi ^ ksw);
+    unsigned va[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int r = 4 * hi + vj + 8 * e;
+        va[e] = lds0 + C::kTile * 2 + r * kRowB + 16u * (unsigned)chunk_pos<D>(r, vchunk) + 2u * vsub;
+    }
+    copy_tile<D, 0, kW>(off, wave, K + kvhead, V + kvhead, 0, S, lds0);
+    copy_tile<D, 1, kW>(off, wave, K + kvhead, V + kvhead, 0, S, lds0);
     dma_wait_barrier();
 
-    // At D = 256 (one wave per SIMD, registers full) the allocator otherwise parks O in VGPRs
-    // during the QK^T part and copies all 128 accumulators between VGPRs and AGPRs twice per
-    // tile; an empty asm with an AGPR constraint at both ends of the PV block keeps O in
-    // AGPRs, where the MFMAs accumulate directly.
-    auto pin_o = [&]() {
-        if (D == 256) {
-#pragma unroll
-            for (int i = 0; i < C::kDBlocks; ++i) asm volatile("" : "+a"(o[i]));
-        }
-    };
     if constexpr (D <= 128) {
         // Two tiles per trip: the buffer parity u is then a constant in each copy of the
         // body and the LDS addresses of the two buffers differ by an immediate offset instead
@@ -232,33 +263,31 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
             const unsigned nbuf = lds0 + (unsigned)(u ^ 1) * buf_bytes;
             if (k0 >= wave_kv_end) {  // this wave's queries end before the tile: copies only
                 if (more) {
-                    copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
-                    copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                    copy_tile<D, 0, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                    copy_tile<D, 1, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
                 }
             } else {
-                const half_t* Kt = lds + u * 2 * C::kTile;
-                const half_t* Vt = Kt + C::kTile;
+                const unsigned ubase = (unsigned)u * buf_bytes;
+                // The XORed addresses are recomputed next to their reads in each tile (one VALU
+                // op each) instead of being held: the empty asm hides that they repeat.
+                asm volatile("" : "+v"(ka), "+v"(va[0]), "+v"(va[1]));
                 // ---- S^T = K Q^T for two 32-key blocks, the two accumulator chains interleaved;
                 // the first half of the next tile's copies goes out halfway ----
                 float16_t s[2] = {float16_t{}, float16_t{}};
-                const half_t* kr0 = Kt + krow * D;
-                const half_t* kr1 = kr0 + 32 * D;
 #pragma unroll
                 for (int kk = 0; kk < C::kKSteps; ++kk) {
-                    const int cofs = ((2 * kk + hi) ^ ksw) * 8;
-                    s[0] = mfma32(*reinterpret_cast<const half8_t*>(kr0 + cofs), qf[kk], s[0]);
-                    s[1] = mfma32(*reinterpret_cast<const half8_t*>(kr1 + cofs), qf[kk], s[1]);
+                    const unsigned a = (ka ^ (32u * kk)) + ubase;
+                    s[0] = mfma32(lds_read_b128(a), qf[kk], s[0]);
+                    s[1] = mfma32(lds_read_b128(a + 32 * kRowB), qf[kk], s[1]);
                     if (kk == C::kKSteps / 2 - 1 && more)
-                        copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                        copy_tile<D, 0, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
                 }
                 // V^T operands of the first key step, read now so that their LDS time runs under
                 // the softmax (V does not depend on P); a wave reads transposed V at ~18 B/clk.
                 auto read_v = [&](int ks, int db) {
-                    const int r0 = 16 * ks + 4 * hi + vj;  // e = 0 row
-                    const int r1 = r0 + 8;                 // e = 1 row
-                    const int ch = 4 * db + vchunk;
-                    const half4_t lo = lds_read_tr16(Vt + r0 * D + chunk_pos<D>(r0, ch) * 8 + vsub);
-                    const half4_t up = lds_read_tr16(Vt + r1 * D + chunk_pos<D>(r1, ch) * 8 + vsub);
+                    const unsigned o = ubase + (unsigned)(32 * D * ks);
+                    const half4_t lo = lds_read_tr16_at((va[0] ^ (64u * db)) + o);
+                    const half4_t up = lds_read_tr16_at((va[1] ^ (64u * db)) + o);
                     return half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
                 };
                 half8_t v0[C::kDBlocks];
@@ -266,12 +295,17 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                 for (int db = 0; db < C::kDBlocks; ++db) v0[db] = read_v(0, db);
                 // ---- masks: causal diagonal and keys past S ----
                 if ((kCausal && k0 + kKRows - 1 > qw0) || k0 + kKRows > S) {
+                    // register r of block kb holds key k0 + 4 hi + c, c = 32 kb + 8 (r / 4) + r % 4:
+                    // compare the constant c against per-lane limits
+                    const int base = k0 + 4 * hi;
+                    const int lim_q = kCausal ? my_q - base : INT_MAX;  // masked when c > lim_q
+                    const int lim_s = S - base;                         // masked when c >= lim_s
 #pragma unroll
                     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
-                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                            if ((kCausal && key > my_q) || key >= S) s[kb][r] = -INFINITY;
+                            const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
+                            if (c > lim_q || c >= lim_s) s[kb][r] = -INFINITY;
                         }
                 }
                 // ---- online softmax (exp2 domain), as in the loop below ----
@@ -309,7 +343,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
                     if (ks == 1 && more)
-                        copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                        copy_tile<D, 1, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
 #pragma unroll
                     for (int db = 0; db < C::kDBlocks; ++db)
                         o[db] = mfma32(ks == 0 ? v0[db] : read_v(ks, db), p[ks], o[db]);
@@ -321,38 +355,33 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
         }
     } else {
         for (int t = 0; t < n_tiles; ++t) {
-            pin_o();
             const int k0 = t * kKRows;
             const bool more = t + 1 < n_tiles;
             const unsigned nbuf = lds0 + ((t + 1) & 1) * buf_bytes;
             if (k0 >= wave_kv_end) {  // this wave's queries end before the tile: copies only
                 if (more) {
-                    copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
-                    copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                    copy_tile<D, 0, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                    copy_tile<D, 1, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
                 }
             } else {
-                const half_t* Kt = lds + (t & 1) * 2 * C::kTile;
-                const half_t* Vt = Kt + C::kTile;
+                const unsigned ubase = (unsigned)(t & 1) * buf_bytes;
+                asm volatile("" : "+v"(ka), "+v"(va[0]), "+v"(va[1]));
                 // ---- S^T = K Q^T for two 32-key blocks, the two accumulator chains interleaved ----
-                // K operand reads: at D = 256 (one wave per SIMD, nothing else on the SIMD to run
-                // while a wave waits on LDS) they run kPreK k-steps ahead of their MFMAs, pinned
+                // K operand reads: at D = 256 they run kPreK k-steps ahead of their MFMAs, pinned
                 // there by scheduling barriers, and the first half of the next tile's copies moves
-                // to the top so that the whole QK^T block is one basic block the reads can cross.
-                // Measured on the gated GQA layer: 1.15 vs 1.23 ms causal, +8 % non-causal; at
-                // D <= 128 (two waves per SIMD) the read-ahead measured no change.
-                constexpr int kPreK = D == 256 ? 4 : 1;
+                // to the top so that the whole QK^T block is one basic block the reads can cross
+                // (2 ahead: with two waves per SIMD the registers allow no more).  At D <= 128
+                // the read-ahead measured no change.
+                constexpr int kPreK = D == 256 ? 2 : 1;
                 constexpr bool kCopyTop = kPreK > 1;
                 if (kCopyTop && more)
-                    copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                    copy_tile<D, 0, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
                 float16_t s[2] = {float16_t{}, float16_t{}};
-                const half_t* kr0 = Kt + krow * D;
-                const half_t* kr1 = kr0 + 32 * D;
-
-                half8_t ka[C::kKSteps][2];
+                half8_t kop[C::kKSteps][2];
                 auto read_k = [&](int kk) {
-                    const int cofs = ((2 * kk + hi) ^ ksw) * 8;
-                    ka[kk][0] = *reinterpret_cast<const half8_t*>(kr0 + cofs);
-                    ka[kk][1] = *reinterpret_cast<const half8_t*>(kr1 + cofs);
+                    const unsigned a = (ka ^ (32u * kk)) + ubase;
+                    kop[kk][0] = lds_read_b128(a);
+                    kop[kk][1] = lds_read_b128(a + 32 * kRowB);
                 };
     #pragma unroll
                 for (int kk = 0; kk < kPreK; ++kk) read_k(kk);
@@ -360,22 +389,20 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     #pragma unroll
                 for (int kk = 0; kk < C::kKSteps; ++kk) {
                     if (kk + kPreK < C::kKSteps) read_k(kk + kPreK);
-                    s[0] = mfma32(ka[kk][0], qf[kk], s[0]);
-                    s[1] = mfma32(ka[kk][1], qf[kk], s[1]);
+                    s[0] = mfma32(kop[kk][0], qf[kk], s[0]);
+                    s[1] = mfma32(kop[kk][1], qf[kk], s[1]);
                     if (kPreK > 1) __builtin_amdgcn_sched_barrier(0);
                     if (!kCopyTop && kk == C::kKSteps / 2 - 1 && more)
-                        copy_tile<D, 0>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                        copy_tile<D, 0, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
                 }
                 // V^T operands of the first key step, read now so that their LDS time runs under
                 // the softmax (V does not depend on P); a wave reads transposed V at only ~18 B/clk.
                 // At D = 256 the registers are not there (one wave per SIMD already).
                 constexpr bool kPreV = D <= 128;
                 auto read_v = [&](int ks, int db) {
-                    const int r0 = 16 * ks + 4 * hi + vj;      // e = 0 row
-                    const int r1 = r0 + 8;                       // e = 1 row
-                    const int ch = 4 * db + vchunk;
-                    const half4_t lo = lds_read_tr16(Vt + r0 * D + chunk_pos<D>(r0, ch) * 8 + vsub);
-                    const half4_t up = lds_read_tr16(Vt + r1 * D + chunk_pos<D>(r1, ch) * 8 + vsub);
+                    const unsigned o = ubase + (unsigned)(32 * D * ks);
+                    const half4_t lo = lds_read_tr16_at((va[0] ^ (64u * db)) + o);
+                    const half4_t up = lds_read_tr16_at((va[1] ^ (64u * db)) + o);
                     return half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
                 };
                 half8_t v0[kPreV ? C::kDBlocks : 1];
@@ -385,12 +412,17 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                 }
                 // ---- masks: causal diagonal and keys past S ----
                 if ((kCausal && k0 + kKRows - 1 > qw0) || k0 + kKRows > S) {
-    #pragma unroll
+                    // register r of block kb holds key k0 + 4 hi + c, c = 32 kb + 8 (r / 4) + r % 4:
+                    // compare the constant c against per-lane limits
+                    const int base = k0 + 4 * hi;
+                    const int lim_q = kCausal ? my_q - base : INT_MAX;  // masked when c > lim_q
+                    const int lim_s = S - base;                         // masked when c >= lim_s
+#pragma unroll
                     for (int kb = 0; kb < 2; ++kb)
-    #pragma unroll
+#pragma unroll
                         for (int r = 0; r < 16; ++r) {
-                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                            if ((kCausal && key > my_q) || key >= S) s[kb][r] = -INFINITY;
+                            const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
+                            if (c > lim_q || c >= lim_s) s[kb][r] = -INFINITY;
                         }
                 }
                 // ---- online softmax (exp2 domain) ----
@@ -432,14 +464,13 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
                     if (ks == 1 && more)
-                        copy_tile<D, 1>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                        copy_tile<D, 1, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
     #pragma unroll
                     for (int db = 0; db < C::kDBlocks; ++db)
                         o[db] = mfma32(kPreV && ks == 0 ? v0[kPreV ? db : 0] : read_v(ks, db), p[ks], o[db]);
                 }
                 __builtin_amdgcn_s_setprio(0);
-                pin_o();
-            }
+                }
             dma_wait_barrier();
         }
     }
@@ -471,10 +502,10 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
 template <int D, bool kCausal>
 hipError_t launch(const half_t* q, const half_t* k, const half_t* v, const half_t* gate, half_t* o,
                   int B, int Hq, int Hkv, int S, float scale, hipStream_t stream) {
+    constexpr int kW = D == 256 ? 8 : 4;
     const int BH = B * Hq;
-    const int n_qt = (S + kQRows - 1) / kQRows;
-    const int lds = Cfg<D>::kLdsBytes;
-    hipLaunchKernelGGL((attn_fwd_kernel<D, kCausal>), dim3(BH * n_qt), dim3(kThreads), lds,
+    const int n_qt = (S + 32 * kW - 1) / (32 * kW);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, kCausal, kW>), dim3(BH * n_qt), dim3(64 * kW), 0,
                        stream, q, k, v, gate, o, S, BH, n_qt, Hq, Hq / Hkv, scale * kLog2e);
     return hipGetLastError();
 }
