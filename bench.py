@@ -18,10 +18,11 @@ cycling the 16 replicas, between one pair of events (a serving loop's step time,
 launch's latency); the 16 in-step launches are reported beside it.
 W untimed warmup steps (default 50, grouped by part with attention last: the board's power
 management needs ~12 ms of continuous attention to settle), then exactly K timed steps
-between two synchronisations, their work grouped by part (K attention launches back to back, then K prefills, then the K x 16
-decode launches), so each kernel is timed in its own loop as the reference's lab drivers
-time theirs.  Each kernel's average duration comes from HIP events recorded on the stream
-it runs on.
+between two synchronisations, their work grouped by part (K attention launches back to
+back, then K prefills, then the K x 16 decode launches), so each kernel is timed in its own
+loop as the reference's lab drivers time theirs: a part's average launch duration is one
+pair of HIP events around its K launches, on the stream they run on, divided by K (the
+prefill's per-call state reset is timed alone the same way and subtracted).
 After the timed steps, outside the step, the gated grouped-query attention layer of the
 reference's target model (B=1, 24 query / 4 K/V heads, D=256, S=8192, causal, gate after
 softmax) is timed on its own and reported as the part `attn_gqa_gated`; so is the GDN
@@ -433,35 +434,33 @@ def main():
     torch.cuda.synchronize()
 
     K = args.steps
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in parts] for _ in range(K)]
-    zero_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(K)]
+    grp = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in parts]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     # The K steps' work grouped by part: K attention launches back to back, then K prefills,
     # then K x 16 decode steps -- each kernel timed in its own loop, as the reference's lab
-    # drivers time theirs (src/attn_sm75.cu:507-519) -- per-launch events on the kernels' stream.
+    # drivers time theirs (src/attn_sm75.cu:507-519): one pair of events on the kernels'
+    # stream around each part's K launches (an event record between launches adds a few
+    # microseconds of barrier to each).
     for j, (name, fn) in enumerate(parts):
+        grp[j][0].record(stream)
         for i in range(K):
-            if name == "gdn_prefill":  # time the state reset separately, it is not the kernel
-                zero_ev[i][0].record(stream)
-                pre["state"].zero_()
-                zero_ev[i][1].record(stream)
-                ev[i][j][0].record(stream)
-                tsa.gdn_chunked_fwd(pre["q"], pre["k"], pre["v"], pre["g"], pre["beta"],
-                                    pre["state"], pre["out"], ws=ws, stream=stream)
-                ev[i][j][1].record(stream)
-            else:
-                ev[i][j][0].record(stream)
-                fn()
-                ev[i][j][1].record(stream)
+            fn()
+        grp[j][1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = {name: sum(ev[i][j][0].elapsed_time(ev[i][j][1]) for i in range(K)) / K
-          for j, (name, _) in enumerate(parts)}
-    ms["gdn_decode"] /= DECODE["replicas"]  # per decode step (one launch)
+    ms = {name: grp[j][0].elapsed_time(grp[j][1]) / K for j, (name, _) in enumerate(parts)}
     ms_step = wall * 1e3 / K
+    # the prefill part resets the state before each call (every step is the same prefill
+    # from a zero state): that reset, timed alone the same way, is not the kernel's
+    z0, z1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    z0.record(stream)
+    for i in range(K):
+        pre["state"].zero_()
+    z1.record(stream)
+    torch.cuda.synchronize()
+    ms["gdn_prefill"] -= z0.elapsed_time(z1) / K
+    ms["gdn_decode"] /= DECODE["replicas"]  # per decode step (one launch)
 
     redo = tsa.gdn_chunked_redo_count(ws, PREFILL["B"], PREFILL["T"], PREFILL["Hq"], PREFILL["Hv"],
                                       stream=stream)

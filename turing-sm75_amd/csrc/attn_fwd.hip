@@ -69,16 +69,19 @@ __device__ __forceinline__ int chunk_pos(int r, int c) {
 }
 
 // Map the linear workgroup id to (bh, query tile).  Workgroups are dispatched round
-// robin over the 8 XCDs; when BH is a multiple of 8, XCD x runs the contiguous heads
-// x * BH/8 .. (x + 1) * BH/8 - 1, so the query heads of one K/V group (adjacent head
-// numbers) share an XCD and read their K/V tiles through the same L2.  Causal runs issue
-// the longest (highest) query tiles first.
-__device__ __forceinline__ void map_block(int bid, int BH, int n_qt, bool causal, int& bh,
-                                          int& qt) {
+// robin over the 8 XCDs; when BH is a multiple of 8 the heads are spread over the XCDs so
+// that all query tiles of a head run on one XCD: with grouped K/V heads (group > 1) XCD x
+// runs the contiguous heads x * BH/8 .. (x + 1) * BH/8 - 1, so the query heads of one K/V
+// group (adjacent head numbers) read their K/V tiles through the same L2 (gated GQA layer:
+// 1.22 -> 0.49 GB of HBM traffic per launch); without groups XCD x runs heads x, x + 8, ...
+// (0.48 vs 0.56 GB at B=1 H=32 S=8192 D=128).  Causal runs issue the longest (highest) query
+// tiles first.
+__device__ __forceinline__ void map_block(int bid, int BH, int n_qt, bool causal, int group,
+                                          int& bh, int& qt) {
     int rank;
     if ((BH & 7) == 0) {
         const int xcd = bid & 7, slot = bid >> 3, hpx = BH >> 3;
-        bh = xcd * hpx + slot % hpx;
+        bh = group > 1 ? xcd * hpx + slot % hpx : (slot % hpx) * 8 + xcd;
         rank = slot / hpx;
     } else {
         bh = bid % BH;
@@ -190,7 +193,7 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hi = lane >> 5;  // which half of the wave
     int bh, qt;
-    map_block(blockIdx.x, BH, n_qt, kCausal, bh, qt);
+    map_block(blockIdx.x, BH, n_qt, kCausal, group, bh, qt);
     const size_t head = (size_t)bh * S * D;  // Q, O, gate: query head bh = b * Hq + h
     const size_t kvhead = (size_t)((bh / Hq) * (Hq / group) + (bh % Hq) / group) * S * D;
     const int q0 = qt * (32 * kW);
