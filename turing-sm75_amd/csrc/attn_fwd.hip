@@ -357,6 +357,9 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
           }
         }
     } else {
+        // D = 256: each 64-key tile is taken as two 32-key halves in turn (S^T of one half: 16
+        // registers), which leaves the registers for K and V^T operand read-ahead beside the
+        // 128 O^T accumulators and the 64 Q operand registers.
         for (int t = 0; t < n_tiles; ++t) {
             const int k0 = t * kKRows;
             const bool more = t + 1 < n_tiles;
@@ -368,112 +371,103 @@ attn_fwd_kernel(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                 }
             } else {
                 const unsigned ubase = (unsigned)(t & 1) * buf_bytes;
-                asm volatile("" : "+v"(ka), "+v"(va[0]), "+v"(va[1]));
-                // ---- S^T = K Q^T for two 32-key blocks, the two accumulator chains interleaved ----
-                // K operand reads: at D = 256 they run kPreK k-steps ahead of their MFMAs, pinned
-                // there by scheduling barriers, and the first half of the next tile's copies moves
-                // to the top so that the whole QK^T block is one basic block the reads can cross
-                // (2 ahead: with two waves per SIMD the registers allow no more).  At D <= 128
-                // the read-ahead measured no change.
-                constexpr int kPreK = D == 256 ? 2 : 1;
-                constexpr bool kCopyTop = kPreK > 1;
-                if (kCopyTop && more)
-                    copy_tile<D, 0, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
-                float16_t s[2] = {float16_t{}, float16_t{}};
-                half8_t kop[C::kKSteps][2];
-                auto read_k = [&](int kk) {
-                    const unsigned a = (ka ^ (32u * kk)) + ubase;
-                    kop[kk][0] = lds_read_b128(a);
-                    kop[kk][1] = lds_read_b128(a + 32 * kRowB);
-                };
-    #pragma unroll
-                for (int kk = 0; kk < kPreK; ++kk) read_k(kk);
-                if (kPreK > 1) __builtin_amdgcn_sched_barrier(0);
-    #pragma unroll
-                for (int kk = 0; kk < C::kKSteps; ++kk) {
-                    if (kk + kPreK < C::kKSteps) read_k(kk + kPreK);
-                    s[0] = mfma32(kop[kk][0], qf[kk], s[0]);
-                    s[1] = mfma32(kop[kk][1], qf[kk], s[1]);
-                    if (kPreK > 1) __builtin_amdgcn_sched_barrier(0);
-                    if (!kCopyTop && kk == C::kKSteps / 2 - 1 && more)
-                        copy_tile<D, 0, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
-                }
-                // V^T operands of the first key step, read now so that their LDS time runs under
-                // the softmax (V does not depend on P); a wave reads transposed V at only ~18 B/clk.
-                // At D = 256 the registers are not there (one wave per SIMD already).
-                constexpr bool kPreV = D <= 128;
-                auto read_v = [&](int ks, int db) {
-                    const unsigned o = ubase + (unsigned)(32 * D * ks);
-                    const half4_t lo = lds_read_tr16_at((va[0] ^ (64u * db)) + o);
-                    const half4_t up = lds_read_tr16_at((va[1] ^ (64u * db)) + o);
-                    return half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-                };
-                half8_t v0[kPreV ? C::kDBlocks : 1];
-                if (kPreV) {
-    #pragma unroll
-                    for (int db = 0; db < C::kDBlocks; ++db) v0[db] = read_v(0, db);
-                }
-                // ---- masks: causal diagonal and keys past S ----
-                if ((kCausal && k0 + kKRows - 1 > qw0) || k0 + kKRows > S) {
-                    // register r of block kb holds key k0 + 4 hi + c, c = 32 kb + 8 (r / 4) + r % 4:
-                    // compare the constant c against per-lane limits
-                    const int base = k0 + 4 * hi;
-                    const int lim_q = kCausal ? my_q - base : INT_MAX;  // masked when c > lim_q
-                    const int lim_s = S - base;                         // masked when c >= lim_s
+                // the first half of the next tile's copies goes out at the top
+                if (more) copy_tile<D, 0, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
+                for (int kb = 0; kb < 2; ++kb) {
+                    const int kb0 = k0 + 32 * kb;  // first key of this half
+                    // a second half wholly past this wave's last query adds nothing
+                    if (kCausal && kb == 1 && kb0 > qw0 + 31) break;
+                    // The XORed addresses are recomputed next to their reads in each half (one
+                    // VALU op each) instead of being held: the empty asm hides that they repeat.
+                    asm volatile("" : "+v"(ka), "+v"(va[0]), "+v"(va[1]));
+                    // ---- S^T = K Q^T for this half: the K operand reads run kPreK k-steps ahead
+                    // of their MFMAs, pinned there by scheduling barriers ----
+                    constexpr int kPreK = 3;
+                    float16_t sh = float16_t{};
+                    half8_t kop[C::kKSteps];
+                    auto read_k = [&](int kk) {
+                        kop[kk] = lds_read_b128((ka ^ (32u * kk)) + ubase + (unsigned)(32 * kb) * kRowB);
+                    };
+#pragma unroll
+                    for (int kk = 0; kk < kPreK; ++kk) read_k(kk);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int kk = 0; kk < C::kKSteps; ++kk) {
+                        if (kk + kPreK < C::kKSteps) read_k(kk + kPreK);
+                        sh = mfma32(kop[kk], qf[kk], sh);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    // ---- masks: causal diagonal and keys past S ----
+                    if ((kCausal && kb0 + 31 > qw0) || kb0 + 32 > S) {
+                        // register r holds key kb0 + 4 hi + c, c = 8 (r / 4) + r % 4: compare the
+                        // constant c against per-lane limits
+                        const int base = kb0 + 4 * hi;
+                        const int lim_q = kCausal ? my_q - base : INT_MAX;  // masked when c > lim_q
+                        const int lim_s = S - base;                         // masked when c >= lim_s
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
-                            const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
-                            if (c > lim_q || c >= lim_s) s[kb][r] = -INFINITY;
+                            const int c = 8 * (r >> 2) + (r & 3);
+                            if (c > lim_q || c >= lim_s) sh[r] = -INFINITY;
                         }
-                }
-                // ---- online softmax (exp2 domain) ----
-                float mx = -INFINITY;
-    #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-    #pragma unroll
-                    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-                mx = max_xor32(mx);
-                // Raise the reference max only when some score would exceed it by 2^8 in the
-                // exp2 domain (always on the first unmasked tile: m = -inf).
-                if (__builtin_amdgcn_ballot_w64((mx - m) * c2 > 8.f)) {
-                    const float m_new = fmaxf(m, mx);
-                    const float alpha = m_new == -INFINITY ? 1.f : fast_exp2((m - m_new) * c2);
-                    m = m_new;
-                    l *= alpha;
-    #pragma unroll
-                    for (int db = 0; db < C::kDBlocks; ++db)
-    #pragma unroll
-                        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-                }
-                const float mc = m == -INFINITY ? 0.f : m * c2;
-                half8_t p[4];
-    #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-    #pragma unroll
+                    }
+                    // ---- online softmax (exp2 domain) ----
+                    float mx = sh[0];
+#pragma unroll
+                    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sh[r]);
+                    mx = max_xor32(mx);
+                    // Raise the reference max only when some score would exceed it by 2^8 in the
+                    // exp2 domain (always on the first unmasked half: m = -inf).
+                    if (__builtin_amdgcn_ballot_w64((mx - m) * c2 > 8.f)) {
+                        const float m_new = fmaxf(m, mx);
+                        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2((m - m_new) * c2);
+                        m = m_new;
+                        l *= alpha;
+#pragma unroll
+                        for (int db = 0; db < C::kDBlocks; ++db)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                    }
+                    const float mc = m == -INFINITY ? 0.f : m * c2;
+                    half8_t p[2];
+#pragma unroll
                     for (int r = 0; r < 16; ++r)
-                        p[2 * kb + (r >> 3)][r & 7] = (half_t)fast_exp2(fmaf(s[kb][r], c2, -mc));
-                // row sum of the fp16 P that multiplies V, on v_dot2_f32_f16
-                const half2_t one2 = {(half_t)1.f, (half_t)1.f};
-    #pragma unroll
-                for (int i = 0; i < 4; ++i)
-    #pragma unroll
-                    for (int u = 0; u < 4; ++u)
-                        l = __builtin_amdgcn_fdot2(half2_t{p[i][2 * u], p[i][2 * u + 1]}, one2, l, false);
-                // ---- O^T += V^T P^T (raised priority: the other wave of the SIMD is then mostly in
-                // its QK^T / softmax part, whose instructions fill the gaps between these MFMAs) ----
-                __builtin_amdgcn_s_setprio(1);
-    #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    if (ks == 1 && more)
-                        copy_tile<D, 1, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
-    #pragma unroll
-                    for (int db = 0; db < C::kDBlocks; ++db)
-                        o[db] = mfma32(kPreV && ks == 0 ? v0[kPreV ? db : 0] : read_v(ks, db), p[ks], o[db]);
+                        p[r >> 3][r & 7] = (half_t)fast_exp2(fmaf(sh[r], c2, -mc));
+                    // row sum of the fp16 P that multiplies V, on v_dot2_f32_f16
+                    const half2_t one2 = {(half_t)1.f, (half_t)1.f};
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+                            l = __builtin_amdgcn_fdot2(half2_t{p[i][2 * u], p[i][2 * u + 1]}, one2, l, false);
+                    // ---- O^T += V^T P^T for this half's two key steps (raised priority: the
+                    // other wave of the SIMD is then mostly in its QK^T / softmax part).  The V^T
+                    // operand reads run kPreV steps ahead of their MFMAs, pinned there ----
+                    auto read_v = [&](int ks, int db) {
+                        const unsigned o = ubase + (unsigned)(32 * D * ks);
+                        const half4_t lo = lds_read_tr16_at((va[0] ^ (64u * db)) + o);
+                        const half4_t up = lds_read_tr16_at((va[1] ^ (64u * db)) + o);
+                        return half8_t{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+                    };
+                    __builtin_amdgcn_sched_barrier(0);
+                    __builtin_amdgcn_s_setprio(1);
+                    constexpr int kSteps = 2 * C::kDBlocks, kPreV = 2;
+                    half8_t vbuf[kSteps];
+#pragma unroll
+                    for (int i = 0; i < kPreV; ++i) vbuf[i] = read_v(2 * kb + i / C::kDBlocks, i % C::kDBlocks);
+#pragma unroll
+                    for (int i = 0; i < kSteps; ++i) {
+                        const int ks = i / C::kDBlocks, db = i % C::kDBlocks;
+                        if (i + kPreV < kSteps)
+                            vbuf[i + kPreV] = read_v(2 * kb + (i + kPreV) / C::kDBlocks, (i + kPreV) % C::kDBlocks);
+                        if (kb == 0 && i == C::kDBlocks && more)
+                            copy_tile<D, 1, kW>(off, wave, K + kvhead, V + kvhead, k0 + kKRows, S, nbuf);
+                        o[db] = mfma32(vbuf[i], p[ks], o[db]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    __builtin_amdgcn_s_setprio(0);
                 }
-                __builtin_amdgcn_s_setprio(0);
-                }
+            }
             dma_wait_barrier();
         }
     }
