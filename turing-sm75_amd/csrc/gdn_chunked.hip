@@ -202,20 +202,38 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
     unsigned char* wsc = ws + ((size_t)bh * nch + ch) * ws_chunk<kF32>();
     const int mt = wave >> 1, nt = wave & 1;  // this wave's 32x32 tile of K K^T / Q K^T
 
-    // ---- 1. K rows to LDS, V rows and this wave's Q operand rows to registers ----
-    uint4 vreg[4];
+    // ---- 1. K rows to LDS, V rows and this wave's Q operand rows to registers.  Every global
+    // load of the phase is issued first (wave 0's gate inputs, K, V, Q), from row-clamped
+    // addresses, and rows past T are zeroed where the values are consumed: a branch around a
+    // load makes the compiler wait for every load in flight where the paths join, which had
+    // serialised the phase into one memory latency per K row group ----
+    const int lastt = T - 1;
+    float gx = 0.f, gy = 0.f;  // wave 0: the gate inputs of token t0 + lane
+    if (wave == 0) {
+        const size_t bt = (size_t)b * T + min(t0 + lane, lastt);
+        gx = kFused ? gates.a[bt * Hv + h] : g_log[bt * Hv + h];
+        gy = kFused ? gates.b[bt * Hv + h] : beta[bt * Hv + h];
+    }
+    uint4 kreg[4], vreg[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int id = it * kThreads + tid;
+        const size_t bt = (size_t)b * T + min(t0 + (id >> 4), lastt);
+        kreg[it] = load8h(k + (bt * Hq + hq) * kD + (id & 15) * 8);
+        vreg[it] = load8h(v + (bt * Hv + h) * kD + (id & 15) * 8);
+    }
+    half8_t qa[kD / 16];
+    const int qt_row = t0 + 32 * mt + (lane & 31);
+    {
+        const TIO* qrow = q + (((size_t)b * T + min(qt_row, lastt)) * Hq + hq) * kD + 8 * hi;
+#pragma unroll
+        for (int s = 0; s < kD / 16; ++s) qa[s] = __builtin_bit_cast(half8_t, load8h(qrow + 16 * s));
+    }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int id = it * kThreads + tid;
         const int r = id >> 4, c = id & 15;
-        const int tt = t0 + r;
-        uint4 kv = make_uint4(0, 0, 0, 0);
-        vreg[it] = kv;
-        if (tt < T) {
-            const size_t bt = (size_t)b * T + tt;
-            kv = load8h(k + (bt * Hq + hq) * kD + c * 8);
-            vreg[it] = load8h(v + (bt * Hv + h) * kD + c * 8);
-        }
+        const uint4 kv = t0 + r > lastt ? make_uint4(0, 0, 0, 0) : kreg[it];
         *reinterpret_cast<uint4*>(sm.K + tile_off(r, c)) = kv;
         if (kF32) store_dev(wsc + kWsK + (size_t)(r * kD + c * 8) * 2, kv);
         if (kFused) {  // the row's 16 threads are 16 consecutive lanes of one wave
@@ -230,13 +248,9 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
             if (c == 0) sm.kn[r] = 1.f / fmaxf(sqrtf(ss), gates.eps);
         }
     }
-    half8_t qa[kD / 16];
     {
-        const int tt = t0 + 32 * mt + (lane & 31);
-        const TIO* qrow = q + (((size_t)b * T + tt) * Hq + hq) * kD + 8 * hi;
 #pragma unroll
-        for (int s = 0; s < kD / 16; ++s)
-            qa[s] = tt < T ? __builtin_bit_cast(half8_t, load8h(qrow + 16 * s)) : half8_t{};
+        for (int s = 0; s < kD / 16; ++s) qa[s] = qt_row > lastt ? half8_t{} : qa[s];
         if (kF32 && nt == 0) {  // waves 0 and 2 hold the chunk's 64 Q rows
             const int row = 32 * mt + (lane & 31);
 #pragma unroll
@@ -254,16 +268,14 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
         }
     }
     if (wave == 0) {
-        const int tt = t0 + lane;
-        const size_t bt = (size_t)b * T + tt;
         float x = 0.f, be = 0.f;
-        if (tt < T) {
+        if (t0 + lane <= lastt) {
             if (kFused) {
-                x = gdn_softplus(gates.a[bt * Hv + h] + gates.dt_bias[h]) * gates.A[h];
-                be = gdn_sigmoid(gates.b[bt * Hv + h]);
+                x = gdn_softplus(gx + gates.dt_bias[h]) * gates.A[h];
+                be = gdn_sigmoid(gy);
             } else {
-                x = g_log[bt * Hv + h];
-                be = beta[bt * Hv + h];
+                x = gx;
+                be = gy;
             }
         }
 #pragma unroll
@@ -442,9 +454,10 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
         }
         lds_barrier();
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
+        for (int it = 0; it < 4; ++it) {  // V rows past T (loaded from the last row) are zero
             const int id = it * kThreads + tid;
-            *reinterpret_cast<uint4*>(sm.x.V + tile_off(id >> 4, id & 15)) = vreg[it];
+            *reinterpret_cast<uint4*>(sm.x.V + tile_off(id >> 4, id & 15)) =
+                t0 + (id >> 4) > lastt ? make_uint4(0, 0, 0, 0) : vreg[it];
         }
         lds_barrier();
 #pragma unroll
