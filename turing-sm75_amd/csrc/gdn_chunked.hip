@@ -190,7 +190,7 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
                const TIO* __restrict__ v, const float* __restrict__ g_log,
                const float* __restrict__ beta, GdnRawGates gates, unsigned char* __restrict__ ws,
                unsigned* __restrict__ flags, int T, int Hq, int Hv, int nch, int BHv) {
-    __shared__ PrepLds sm;
+    __shared__ __align__(16) PrepLds sm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hi = lane >> 5;
     // chunk-major: workgroups are dispatched in the order the carry consumes chunks, and
     // (b, h, chunk) lands on the XCD of the head's carry workgroups when BHv % 8 == 0
@@ -310,17 +310,35 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
         const float Gs = sm.G[rb];
         const float kns = kFused ? sm.kn[rb] : 1.f;
         const int sp = perm32(rb);
+        // this lane's rows t = 32mt + 8q + 4hi + 0..3: four 16-byte reads per factor (one
+        // 4-byte read per row had made this phase a chain of ~65 small LDS round trips)
+        float4 g4[4], b4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int t0q = 32 * mt + 8 * q + 4 * hi;
+            g4[q] = *reinterpret_cast<const float4*>(sm.G + t0q);
+            b4[q] = *reinterpret_cast<const float4*>(sm.bt + t0q);
+        }
+        // A is stored only for blocks (t/16, rb/16) on or below the diagonal; in the one block
+        // above it (mt == nt, rb in the upper half, t in the lower) the lane writes a slot of
+        // sm.bg instead (rewritten in phase 3), so no store needs a branch.  Entries with
+        // rb >= t inside stored diagonal blocks get zeros, which nothing reads.
+        const bool upper = mt == nt && ((lane >> 4) & 1);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int t = 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
-            const float dec = (rb <= t) ? __expf(sm.G[t] - Gs) : 0.f;
-            if (kFused) {
-                if (rb < t) sm.x.s.A[tri_off(t, rb)] = sm.bt[t] * kk[r] * (dec * sm.kn[t] * kns);
-                sm.x.s.Aqk[t * kC + sp] = (half_t)(qk[r] * (dec * sm.qn[t] * kns));
-            } else {
-                if (rb < t) sm.x.s.A[tri_off(t, rb)] = sm.bt[t] * kk[r] * dec;
-                sm.x.s.Aqk[t * kC + sp] = (half_t)(qk[r] * dec);
+            const int q = r >> 2, e = r & 3;
+            const int t = 32 * mt + 8 * q + 4 * hi + e;
+            const float Gt = e == 0 ? g4[q].x : e == 1 ? g4[q].y : e == 2 ? g4[q].z : g4[q].w;
+            const float bt = e == 0 ? b4[q].x : e == 1 ? b4[q].y : e == 2 ? b4[q].z : b4[q].w;
+            const float dec = (rb <= t) ? __expf(Gt - Gs) : 0.f;
+            float aval = bt * kk[r] * dec, qval = qk[r] * dec;
+            if (kFused) {  // per-row reads here: 16-byte ones would hold 32 more registers
+                aval = bt * kk[r] * (dec * sm.kn[t] * kns);
+                qval = qk[r] * (dec * sm.qn[t] * kns);
             }
+            float* ap = (upper && r < 8) ? sm.bg + (lane & 63) : sm.x.s.A + tri_off(t, rb);
+            *ap = rb < t ? aval : 0.f;
+            sm.x.s.Aqk[t * kC + sp] = (half_t)qval;
         }
     }
     lds_barrier();
