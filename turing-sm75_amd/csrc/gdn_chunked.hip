@@ -316,8 +316,10 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int t0q = 32 * mt + 8 * q + 4 * hi;
-            g4[q] = *reinterpret_cast<const float4*>(sm.G + t0q);
-            b4[q] = *reinterpret_cast<const float4*>(sm.bt + t0q);
+            if (!kFused) {
+                g4[q] = *reinterpret_cast<const float4*>(sm.G + t0q);
+                b4[q] = *reinterpret_cast<const float4*>(sm.bt + t0q);
+            }
         }
         // A is stored only for blocks (t/16, rb/16) on or below the diagonal; in the one block
         // above it (mt == nt, rb in the upper half, t in the lower) the lane writes a slot of
@@ -328,8 +330,9 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
         for (int r = 0; r < 16; ++r) {
             const int q = r >> 2, e = r & 3;
             const int t = 32 * mt + 8 * q + 4 * hi + e;
-            const float Gt = e == 0 ? g4[q].x : e == 1 ? g4[q].y : e == 2 ? g4[q].z : g4[q].w;
-            const float bt = e == 0 ? b4[q].x : e == 1 ? b4[q].y : e == 2 ? b4[q].z : b4[q].w;
+            // the fused variant reads per row (holding the 32 values spills it)
+            const float Gt = kFused ? sm.G[t] : e == 0 ? g4[q].x : e == 1 ? g4[q].y : e == 2 ? g4[q].z : g4[q].w;
+            const float bt = kFused ? sm.bt[t] : e == 0 ? b4[q].x : e == 1 ? b4[q].y : e == 2 ? b4[q].z : b4[q].w;
             const float dec = (rb <= t) ? __expf(Gt - Gs) : 0.f;
             float aval = bt * kk[r] * dec, qval = qk[r] * dec;
             if (kFused) {  // per-row reads here: 16-byte ones would hold 32 more registers
