@@ -5,8 +5,8 @@
 //         g_log = softplus(a + dt_bias[h]) * A[h]   (A = -exp(A_log), per V-head)
 //   post: y = x / sqrt(mean(x^2) + eps) * w * silu(z)   per (token, V-head) row
 // All are HBM-bound streams of 256-byte rows: a row belongs to 16 lanes that each move 16
-// bytes, so every instruction covers whole 128-byte lines, and the row sums are 4 lane
-// exchanges inside the 16-lane group.  The fused prefill / decode entry points apply the
+// bytes, so every instruction covers whole 128-byte lines, and the row sums are 4 DPP
+// steps inside the 16-lane group.  The fused prefill / decode entry points apply the
 // pre-ops inside the recurrence kernels instead (gdn_chunked.hip, gdn_recurrent.hip).
 #include "common.h"
 #include "kernels.h"
@@ -17,12 +17,11 @@ namespace {
 constexpr int kD = 128;
 constexpr int kRowsPerBlock = 16;  // 256 threads, 16 per row
 
-__device__ __forceinline__ float sum16(float x) {
-    x += __shfl_xor(x, 8);
-    x += __shfl_xor(x, 4);
-    x += __shfl_xor(x, 2);
-    x += __shfl_xor(x, 1);
-    return x;
+// Sum over each aligned group of 16 lanes by DPP (no LDS round trip): the 8-lane sums, then
+// each lane adds the mirror lane of the other half of its row.
+__device__ __forceinline__ float sum16_dpp(float x) {
+    x = sum8(x);
+    return x + dpp_mov<kDppRowMirror>(x);
 }
 
 // Rows [0, rows) of x0 and then rows [0, rows) of x1, normalised into y0 / y1.
@@ -40,7 +39,7 @@ l2norm_rows_kernel(const half_t* x0, half_t* y0, const half_t* x1,  // y may ali
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss = fmaf((float)v[e], (float)v[e], ss);
-    const float inv = 1.f / fmaxf(sqrtf(sum16(ss)), eps);
+    const float inv = 1.f / fmaxf(sqrtf(sum16_dpp(ss)), eps);
     half8_t o;
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = (half_t)((float)v[e] * inv);
@@ -58,28 +57,44 @@ gdn_gates_kernel(const float* __restrict__ a, const float* __restrict__ b,
     beta[i] = gdn_sigmoid(b[i]);
 }
 
+// silu(z) = z sigmoid(z) on the hardware exp2 and reciprocal (both ~1 ulp): for z below
+// about -88 the exponential is +inf and the result the limit -0.
+__device__ __forceinline__ float silu_fast(float z) {
+    return z * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-z * kLog2e));
+}
+
+// kRmsRows rows per thread group of 16: every row's x and z loads are issued before any is
+// used (rows past the end clamped to the last row, their results not stored), so each
+// thread keeps 2 kRmsRows 16-byte loads in flight instead of 2.
+constexpr int kRmsRows = 4;
+
 __global__ void __launch_bounds__(256)
 gated_rmsnorm_kernel(const half_t* x, const half_t* __restrict__ z,
                      const float* __restrict__ w, half_t* y, long long rows, float eps) {  // y may alias x
-    const long long r = (long long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
-    if (r >= rows) return;
+    const long long r0 = (long long)blockIdx.x * (kRowsPerBlock * kRmsRows) + (threadIdx.x >> 4);
     const int c = threadIdx.x & 15;
-    const half8_t xv = *reinterpret_cast<const half8_t*>(x + r * kD + 8 * c);
-    const half8_t zv = *reinterpret_cast<const half8_t*>(z + r * kD + 8 * c);
+    half8_t xv[kRmsRows], zv[kRmsRows];
+#pragma unroll
+    for (int i = 0; i < kRmsRows; ++i) {
+        const long long r = min(r0 + (long long)kRowsPerBlock * i, rows - 1);
+        xv[i] = *reinterpret_cast<const half8_t*>(x + r * kD + 8 * c);
+        zv[i] = *reinterpret_cast<const half8_t*>(z + r * kD + 8 * c);
+    }
     const float4 w0 = *reinterpret_cast<const float4*>(w + 8 * c);
     const float4 w1 = *reinterpret_cast<const float4*>(w + 8 * c + 4);
     const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-    float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf((float)xv[e], (float)xv[e], ss);
-    const float rs = 1.f / sqrtf(sum16(ss) * (1.f / kD) + eps);
-    half8_t o;
+    for (int i = 0; i < kRmsRows; ++i) {
+        float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float zf = (float)zv[e];
-        o[e] = (half_t)((float)xv[e] * rs * wv[e] * (zf * gdn_sigmoid(zf)));
+        for (int e = 0; e < 8; ++e) ss = fmaf((float)xv[i][e], (float)xv[i][e], ss);
+        const float rs = 1.f / sqrtf(sum16_dpp(ss) * (1.f / kD) + eps);
+        half8_t o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (half_t)((float)xv[i][e] * rs * wv[e] * silu_fast((float)zv[i][e]));
+        const long long r = r0 + (long long)kRowsPerBlock * i;
+        if (r < rows) *reinterpret_cast<half8_t*>(y + r * kD + 8 * c) = o;
     }
-    *reinterpret_cast<half8_t*>(y + r * kD + 8 * c) = o;
 }
 
 }  // namespace
@@ -104,7 +119,7 @@ hipError_t gdn_preprocess(const void* q, const void* k, const float* a, const fl
 hipError_t gdn_gated_rmsnorm(const void* x, const void* z, const float* w, void* y, int B, int T,
                              int Hv, float eps, hipStream_t stream) {
     const long long rows = (long long)B * T * Hv;
-    const long long nb = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    const long long nb = (rows + kRowsPerBlock * kRmsRows - 1) / (kRowsPerBlock * kRmsRows);
     hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3((unsigned)nb), dim3(256), 0, stream,
                        static_cast<const half_t*>(x), static_cast<const half_t*>(z), w,
                        static_cast<half_t*>(y), rows, eps);
