@@ -16,6 +16,10 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kRowsPerBlock = 16;  // 256 threads, 16 per row
+// Rows per 16-lane group: every row's loads are issued before any is used (rows past the end
+// clamped to the last row, their results not stored), so a thread keeps kGroupRows 16-byte
+// loads per input in flight instead of one.
+constexpr int kGroupRows = 4;
 
 // Sum over each aligned group of 16 lanes by DPP (no LDS round trip): the 8-lane sums, then
 // each lane adds the mirror lane of the other half of its row.
@@ -28,22 +32,29 @@ __device__ __forceinline__ float sum16_dpp(float x) {
 __global__ void __launch_bounds__(256)
 l2norm_rows_kernel(const half_t* x0, half_t* y0, const half_t* x1,  // y may alias x
                    half_t* y1, long long rows, float eps) {
-    const long long r = (long long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
-    if (r >= 2 * rows) return;  // whole 16-lane groups leave together
+    const long long r0 = (long long)blockIdx.x * (kRowsPerBlock * kGroupRows) + (threadIdx.x >> 4);
     const int c = threadIdx.x & 15;
-    const bool second = r >= rows;
-    const long long rr = second ? r - rows : r;
-    const half_t* x = (second ? x1 : x0) + rr * kD + 8 * c;
-    half_t* y = (second ? y1 : y0) + rr * kD + 8 * c;
-    const half8_t v = *reinterpret_cast<const half8_t*>(x);
-    float ss = 0.f;
+    half8_t v[kGroupRows];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf((float)v[e], (float)v[e], ss);
-    const float inv = 1.f / fmaxf(sqrtf(sum16_dpp(ss)), eps);
-    half8_t o;
+    for (int i = 0; i < kGroupRows; ++i) {
+        const long long r = min(r0 + (long long)kRowsPerBlock * i, 2 * rows - 1);
+        const bool second = r >= rows;
+        v[i] = *reinterpret_cast<const half8_t*>((second ? x1 : x0) + (second ? r - rows : r) * kD + 8 * c);
+    }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = (half_t)((float)v[e] * inv);
-    *reinterpret_cast<half8_t*>(y) = o;
+    for (int i = 0; i < kGroupRows; ++i) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf((float)v[i][e], (float)v[i][e], ss);
+        const float inv = 1.f / fmaxf(sqrtf(sum16_dpp(ss)), eps);
+        half8_t o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (half_t)((float)v[i][e] * inv);
+        const long long r = r0 + (long long)kRowsPerBlock * i;
+        const bool second = r >= rows;
+        if (r < 2 * rows)
+            *reinterpret_cast<half8_t*>((second ? y1 : y0) + (second ? r - rows : r) * kD + 8 * c) = o;
+    }
 }
 
 __global__ void __launch_bounds__(256)
@@ -63,19 +74,15 @@ __device__ __forceinline__ float silu_fast(float z) {
     return z * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-z * kLog2e));
 }
 
-// kRmsRows rows per thread group of 16: every row's x and z loads are issued before any is
-// used (rows past the end clamped to the last row, their results not stored), so each
-// thread keeps 2 kRmsRows 16-byte loads in flight instead of 2.
-constexpr int kRmsRows = 4;
 
 __global__ void __launch_bounds__(256)
 gated_rmsnorm_kernel(const half_t* x, const half_t* __restrict__ z,
                      const float* __restrict__ w, half_t* y, long long rows, float eps) {  // y may alias x
-    const long long r0 = (long long)blockIdx.x * (kRowsPerBlock * kRmsRows) + (threadIdx.x >> 4);
+    const long long r0 = (long long)blockIdx.x * (kRowsPerBlock * kGroupRows) + (threadIdx.x >> 4);
     const int c = threadIdx.x & 15;
-    half8_t xv[kRmsRows], zv[kRmsRows];
+    half8_t xv[kGroupRows], zv[kGroupRows];
 #pragma unroll
-    for (int i = 0; i < kRmsRows; ++i) {
+    for (int i = 0; i < kGroupRows; ++i) {
         const long long r = min(r0 + (long long)kRowsPerBlock * i, rows - 1);
         xv[i] = *reinterpret_cast<const half8_t*>(x + r * kD + 8 * c);
         zv[i] = *reinterpret_cast<const half8_t*>(z + r * kD + 8 * c);
@@ -84,7 +91,7 @@ gated_rmsnorm_kernel(const half_t* x, const half_t* __restrict__ z,
     const float4 w1 = *reinterpret_cast<const float4*>(w + 8 * c + 4);
     const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-    for (int i = 0; i < kRmsRows; ++i) {
+    for (int i = 0; i < kGroupRows; ++i) {
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss = fmaf((float)xv[i][e], (float)xv[i][e], ss);
@@ -104,7 +111,7 @@ hipError_t gdn_preprocess(const void* q, const void* k, const float* a, const fl
                           float* g_log, float* beta, int B, int T, int Hq, int Hv, float eps,
                           hipStream_t stream) {
     const long long rows = (long long)B * T * Hq;
-    const long long nb = (2 * rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    const long long nb = (2 * rows + kRowsPerBlock * kGroupRows - 1) / (kRowsPerBlock * kGroupRows);
     hipLaunchKernelGGL(l2norm_rows_kernel, dim3((unsigned)nb), dim3(256), 0, stream,
                        static_cast<const half_t*>(q), static_cast<half_t*>(q_out),
                        static_cast<const half_t*>(k), static_cast<half_t*>(k_out), rows, eps);
@@ -119,7 +126,7 @@ hipError_t gdn_preprocess(const void* q, const void* k, const float* a, const fl
 hipError_t gdn_gated_rmsnorm(const void* x, const void* z, const float* w, void* y, int B, int T,
                              int Hv, float eps, hipStream_t stream) {
     const long long rows = (long long)B * T * Hv;
-    const long long nb = (rows + kRowsPerBlock * kRmsRows - 1) / (kRowsPerBlock * kRmsRows);
+    const long long nb = (rows + kRowsPerBlock * kGroupRows - 1) / (kRowsPerBlock * kGroupRows);
     hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3((unsigned)nb), dim3(256), 0, stream,
                        static_cast<const half_t*>(x), static_cast<const half_t*>(z), w,
                        static_cast<half_t*>(y), rows, eps);
