@@ -169,6 +169,87 @@ def test_ragged_and_head_map(dev, orc, kind, T):
     _check(o, s, o_ref, s_ref, *TOL[kind], label=f"{kind} T={T}")
 
 
+# The sequence split (few heads, many chunks): segments' transition maps run side by side and
+# are combined (state after a segment = Phi state before + Z) before the segments' outputs.
+# TSA_GDN_SEGMENTS: None = the library's choice, "1" = no split, n = n segments.
+SPLIT_CASES = [
+    (1, 4096, 2, 4, None),  # 8 segments of 8 chunks (the library's choice for 4 heads)
+    (1, 1000, 1, 2, "3"),   # 6 + 6 + 4 chunks, the last chunk 40 tokens
+    (2, 777, 3, 4, "5"),    # 3 + 3 + 3 + 3 + 1 chunks, Hv % Hq != 0
+]
+
+
+def _split_ws(monkeypatch, B, T, Hq, Hv, segs, f32=False):
+    """Workspace bytes with and without the split; the split's slots make the first larger,
+    which shows the call takes the split."""
+    monkeypatch.setenv("TSA_GDN_SEGMENTS", "1")
+    plain = tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv, f32=f32)
+    if segs is None:
+        monkeypatch.delenv("TSA_GDN_SEGMENTS")
+    else:
+        monkeypatch.setenv("TSA_GDN_SEGMENTS", segs)
+    return tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv, f32=f32), plain
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "B{}T{}Hq{}Hv{}s{}".format(*c))
+@pytest.mark.parametrize("decay", ["fast", "slow"])
+def test_sequence_split(dev, orc, monkeypatch, case, decay):
+    """Against the oracle, entering with an N(0, 0.02) state.  With the slow gate (about
+    -0.002 per token) the state entering a segment still weighs at its end, so the maps and
+    their combine decide the result; the plain carry on the same inputs passes the same gates."""
+    B, T, Hq, Hv, segs = case
+    rng = np.random.default_rng(T + 7 * Hv)
+    q, k, v, g, beta, st = _inputs(rng, B, T, Hq, Hv, sstd=0.02)
+    if decay == "slow":
+        g = (-0.002 * (1 + 0.5 * rng.standard_normal(g.shape))).astype(np.float32)
+    need, plain = _split_ws(monkeypatch, B, T, Hq, Hv, segs)
+    print(f"split B={B} T={T} Hq={Hq} Hv={Hv} segments={segs} ws {need} (plain {plain})", flush=True)
+    assert need > plain
+    o, s = _gpu(dev, "chunked", q, k, v, g, beta, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    _check(o, s, o_ref, s_ref, *TOL["chunked"], label=f"split {decay}")
+    monkeypatch.setenv("TSA_GDN_SEGMENTS", "1")
+    o1, s1 = _gpu(dev, "chunked", q, k, v, g, beta, st)
+    _check(o1, s1, o_ref, s_ref, *TOL["chunked"], label=f"plain {decay}")
+
+
+def test_sequence_split_fp32_io(dev, orc, monkeypatch):
+    """The split with fp32 I/O (K / Q rows from the prep's fp16 copies in the workspace):
+    4 segments of 5, 5, 5 and 3 chunks."""
+    rng = np.random.default_rng(411)
+    B, T, Hq, Hv = 1, 1100, 2, 4
+    q, k, v, g, beta, st = (a.astype(np.float32) for a in _inputs(rng, B, T, Hq, Hv, sstd=0.02))
+    g = (-0.002 * (1 + 0.5 * rng.standard_normal(g.shape))).astype(np.float32)
+    need, plain = _split_ws(monkeypatch, B, T, Hq, Hv, None, f32=True)
+    print(f"split fp32 I/O ws {need} (plain {plain})", flush=True)
+    assert need > plain
+    o, s = _gpu(dev, "chunked", q, k, v, g, beta, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    _check(o, s, o_ref, s_ref, 2e-3, 8e-4, label="split fp32 I/O")
+
+
+def test_sequence_split_workspace_contents_do_not_matter(dev, monkeypatch):
+    """Every slot of the split is written before it is read: a workspace of 0xff bytes gives
+    the same results bit for bit as a zeroed one."""
+    import torch
+    rng = np.random.default_rng(412)
+    B, T, Hq, Hv = 1, 2048, 2, 4
+    q, k, v, g, beta, st = _inputs(rng, B, T, Hq, Hv, sstd=0.02)
+    need, plain = _split_ws(monkeypatch, B, T, Hq, Hv, None)
+    assert need > plain
+    tq, tk, tv, tg, tb = _dev(dev, q, k, v, g, beta)
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    ts = _dev(dev, st)[0]
+    o0 = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, ws=ws).clone()
+    s0 = ts.clone()
+    ws.fill_(255)
+    ts.copy_(_dev(dev, st)[0])
+    o1 = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, ws=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o0) and torch.equal(ts, s0)
+    assert tsa.gdn_chunked_redo_count(ws, B, T, Hq, Hv) == 0
+
+
 def test_state_continuity_prefill_prefill_decode(dev, orc):
     import torch
     rng = np.random.default_rng(402)

@@ -27,6 +27,8 @@
 //   ahead with gfx950 LDS-DMA (global_load_lds_dwordx4) into double-buffered slots, so no
 //   register holds prefetched data and each wave reads its MFMA operands from LDS in
 //   batches ahead of the MFMAs.
+#include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -60,11 +62,13 @@ constexpr int kWsChunkF32 = kWsQ + kC * kD * 2;  // 91136 B
 template <bool kF32> constexpr int ws_chunk() { return kF32 ? kWsChunkF32 : kWsChunk; }
 
 // Ready flags, after all chunk workspaces: one word per (b, h, chunk), then an abort word per
-// carry workgroup.  Every call first clears them with a small kernel on the caller's stream
-// (gdn_flags_clear, a kernel rather than a memset so that a captured graph replays it
-// correctly), so whatever the workspace held before, no flag reads as set before the prep
-// sets it in this call.  The prep writes 1 there once the chunk's workspace is in memory;
-// the carry's DMA waves wait for it before copying the chunk.
+// carry workgroup.  A call that runs the prep beside the carry first clears them with a small
+// kernel on the caller's stream (gdn_flags_clear, a kernel rather than a memset so that a
+// captured graph replays it correctly), so whatever the workspace held before, no flag reads
+// as set before the prep sets it in this call.  A call that runs them in order needs no clear:
+// its prep has set every flag before the carry starts, and the carry zeroes the abort words
+// itself.  The prep writes 1 there once the chunk's workspace is in memory; the carry's DMA
+// waves wait for it before copying the chunk.
 // A wait gives up after a limit on the 100 MHz real-time counter (2 ms; the environment
 // variable TSA_GDN_CARRY_WAIT_US sets it in microseconds, 0 = give up whenever a chunk is
 // not ready at the first look, which is how the tests exercise the path).  When the prep
@@ -84,6 +88,26 @@ constexpr unsigned kRetryWaitTicks = 100000000u;
 constexpr int kCarryInOrder = 0;  // after the prep on one stream: waits never block
 constexpr int kCarryBeside = 1;   // beside the prep: a timed-out workgroup aborts
 constexpr int kCarryRetry = 2;    // after the prep: only the first launch's aborted workgroups run
+
+// Sequence split (few heads, many chunks): T is cut into nseg segments of seg_len chunks (the
+// last takes the rest).  The state after a segment is an affine map of the state before it,
+// S_out = Phi S_in + Z, where Z is the segment's chain run from S = 0 and Phi its chain run
+// from S = I with U = 0 (the state update is linear in S and in U).  Three launches:
+//   maps   -- segment 0's chain from the caller's state (its outputs, and its end state as
+//             segment 1's entry), and, side by side, Z and Phi of segments 1 .. nseg-2;
+//   combine (gdn_seg_combine) -- entry[s+1] = Phi_s entry[s] + Z_s, s = 1 .. nseg-2;
+//   finish -- segments 1 .. nseg-1 from their entry states, with outputs; the last one's end
+//             state is the call's result.
+// The serial depth drops from nch chunk steps to about 2 seg_len + the combine.  Per (b, h,
+// segment) the workspace holds three [128 columns][128] fp32 slots: entry, Z, Phi.
+constexpr int kJobPlain = 0, kJobMaps = 1, kJobFinish = 2;
+constexpr int kSegSlots = 3, kSegEntry = 0, kSegZ = 1, kSegPhi = 2;
+constexpr size_t kSegSlotFloats = (size_t)kD * kD;
+struct CarryJob {
+    int phase = kJobPlain;
+    int nseg = 1, seg_len = 0;
+    float* seg = nullptr;  // [B*Hv][nseg][kSegSlots][kD][kD]
+};
 
 // Within each aligned 32-block, index 16a + 4g + b is stored at 8g + 4a + b.  A 16x16x32
 // MFMA lane of group g then finds its 8 k-values {16a + 4g + b} in one 16-byte run; that
@@ -732,8 +756,9 @@ __device__ __forceinline__ ChainOffs chain_offs() {
 // operands, U, decay factors) depends only on the chunk's slot, so all of them are issued
 // before the first MFMA and a scheduling barrier keeps them there: the MFMAs then find
 // their operands arriving in order instead of waiting on each small batch.
+// us: 1, or 0 for a transition map's chain (U = 0).
 __device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs, uint4* xs, int sl,
-                                           const ChainOffs& off) {
+                                           const ChainOffs& off, float us) {
     const int lane = threadIdx.x & 63, g = lane >> 4;
     half8_t aW[4][4];
 #pragma unroll
@@ -779,7 +804,7 @@ __device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs
         const float dg[4] = {d4[mt].x, d4[mt].y, d4[mt].z, d4[mt].w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float vn = uu[r] - wsv[mt][r];
+            const float vn = fmaf(uu[r], us, -wsv[mt][r]);
             Vn[mt >> 1][4 * (mt & 1) + r] = (half_t)vn;
             const float vs = vn * dg[r];
             const half_t vh = (half_t)vs;
@@ -880,7 +905,7 @@ __device__ __forceinline__ void out_step(const OutSlot& os, const uint4 (*xs)[6]
 // Called one iteration after out_step, so the stores drain behind a whole iteration of
 // work instead of in front of the next barrier.
 __device__ __forceinline__ void out_flush(const half_t* ostage, half_t* out, int b, int T, int Hv,
-                                          int h, int t0, int pair, int w) {
+                                          int h, int t0, int pair, int w, int Tloc) {
     const int lane = threadIdx.x & 63;
     wave_lds_sync();
 #pragma unroll
@@ -888,7 +913,7 @@ __device__ __forceinline__ void out_flush(const half_t* ostage, half_t* out, int
         const int tl = 16 * hf + (lane >> 2);  // token within this wave's 32
         const int tt = t0 + 32 * w + tl;
         const uint4 v4 = *reinterpret_cast<const uint4*>(ostage + tl * 32 + 8 * (lane & 3));
-        if (tt < T)
+        if (tt < Tloc)
             *reinterpret_cast<uint4*>(out + (((size_t)b * T + tt) * Hv + h) * kD + pair * 32 + 8 * (lane & 3)) = v4;
     }
     wave_lds_sync();
@@ -896,13 +921,16 @@ __device__ __forceinline__ void out_flush(const half_t* ostage, half_t* out, int
 
 // TIO: the q / k / out element type.  With fp32 I/O the K / Q rows come from the prep's fp16
 // copies in the workspace and the output is stored in fp32 straight from registers.
+// job: the whole sequence (kJobPlain), or one launch of the sequence split (segments of the
+// workgroup's unit, its start state and where its end state goes are derived below).
 template <typename TIO>
 __global__ void __launch_bounds__(kCarryThreads, 1)
 gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
                 const unsigned char* __restrict__ ws, const unsigned* __restrict__ flags,
                 unsigned* __restrict__ aborts, int mode, unsigned wait_ticks,
                 float* __restrict__ state,
-                TIO* __restrict__ out, int T, int Hq, int Hv, int nch, int BHv, float scale) {
+                TIO* __restrict__ out, int T, int Hq, int Hv, int nch_all, int BHv, float scale,
+                CarryJob job) {
     constexpr bool kF32 = std::is_same<TIO, float>::value;
     __shared__ CarryLds sm;
     if (mode == kCarryRetry &&
@@ -912,13 +940,48 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: role branches are scalar
     const int g = lane >> 4, c = lane & 15;
-    // block id = pair * BHv + bh: all column pairs of one head share an XCD when BHv % 8 == 0
-    const int pair = blockIdx.x / BHv;
+    // block id = (unit * 4 + pair) * BHv + bh: all column pairs of one head share an XCD when
+    // BHv % 8 == 0
+    const int unit = blockIdx.x / (4 * BHv);
+    const int pair = (blockIdx.x / BHv) & 3;
     const int bh = blockIdx.x % BHv;
     const int b = bh / Hv, h = bh % Hv, hq = h % Hq;
-    const unsigned char* wsh = ws + (size_t)bh * nch * ws_chunk<kF32>();
     const bool chain = wave < 2, outw = wave == 2 || wave == 3, dmaw = wave >= 4;
     const int sl = wave & 1;  // chain wave: its strip; output wave: w = wave - 2
+
+    // This workgroup's chunks [c0, c0 + nch), where its state starts (src: loaded; else zero,
+    // or the identity for a transition map), where it ends (dst, or nowhere), whether it
+    // stores outputs, and the U scale (0 for a transition map).
+    int seg = 0, c0 = 0, nch = nch_all;
+    bool outputs = true, ident = false;
+    float us = 1.f;
+    const float* src = state;
+    float* dst = state;
+    float* segh = job.seg + (size_t)bh * job.nseg * kSegSlots * kSegSlotFloats;  // this head's slots
+    auto slot = [&](int sg, int which) { return segh + ((size_t)sg * kSegSlots + which) * kSegSlotFloats; };
+    if (job.phase == kJobMaps) {
+        if (unit == 0) {            // segment 0 from the caller's state; its end enters segment 1
+            dst = slot(1, kSegEntry);
+        } else {                    // Z or Phi of segment 1 + (unit - 1) / 2
+            seg = 1 + (unit - 1) / 2;
+            const bool phi = ((unit - 1) & 1) != 0;
+            src = nullptr;
+            ident = phi;
+            us = phi ? 0.f : 1.f;
+            dst = slot(seg, phi ? kSegPhi : kSegZ);
+            outputs = false;
+        }
+    } else if (job.phase == kJobFinish) {
+        seg = unit + 1;
+        src = slot(seg, kSegEntry);
+        dst = seg == job.nseg - 1 ? state : nullptr;
+    }
+    if (job.phase != kJobPlain) {
+        c0 = seg * job.seg_len;
+        nch = seg == job.nseg - 1 ? nch_all - c0 : job.seg_len;
+    }
+    const int Tloc = T - c0 * kC;  // tokens from this workgroup's first chunk to the end of the sequence
+    const unsigned char* wsh = ws + ((size_t)bh * nch_all + c0) * ws_chunk<kF32>();
 
     // Pipeline, iteration it.  Chain waves: process chunk it from cs[it&1].  Output waves:
     // store the O tile of chunk it-2 staged in LDS, then compute the output of chunk it-1
@@ -926,12 +989,20 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
     // into cs[(it+1)&1] and the output operands of chunk it into os[it&1], then wait for
     // the copies.  Then the workgroup meets at a barrier.
     float4_t S[8];
-    float* Sg = state + ((size_t)bh * kD + (pair * kStrips + sl) * 16 + c) * kD;
+    // state layout [b*Hv + h][column][dk]: this lane's column, dk rows 16m + 4g + 0..3
+    const int col = (pair * kStrips + sl) * 16 + c;
+    const size_t soff = ((size_t)bh * kD + col) * kD, soff_seg = (size_t)col * kD;
+    const float* Sg = src == state ? state + soff : src + soff_seg;
     if (chain) {
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            const float4 v4 = *reinterpret_cast<const float4*>(Sg + 16 * m + 4 * g);
-            S[m] = float4_t{v4.x, v4.y, v4.z, v4.w};
+            if (src) {
+                const float4 v4 = *reinterpret_cast<const float4*>(Sg + 16 * m + 4 * g);
+                S[m] = float4_t{v4.x, v4.y, v4.z, v4.w};
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) S[m][r] = ident && 16 * m + 4 * g + r == col ? 1.f : 0.f;
+            }
         }
     }
     if (!dmaw) dma_wait_barrier();  // matches the DMA waves' prologue barrier
@@ -941,29 +1012,31 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
     if (chain) {
         const ChainOffs off = chain_offs();
         for (int it = 0; it <= nch; it += 2) {
-            if (it < nch) chain_step(S, sm.cs[0], &sm.XS[0][sl][0][0], sl, off);
+            if (it < nch) chain_step(S, sm.cs[0], &sm.XS[0][sl][0][0], sl, off, us);
             lds_barrier();  // chain waves issue no vector memory operations in the loop
             if (it + 1 > nch) break;
-            if (it + 1 < nch) chain_step(S, sm.cs[1], &sm.XS[1][sl][0][0], sl, off);
+            if (it + 1 < nch) chain_step(S, sm.cs[1], &sm.XS[1][sl][0][0], sl, off, us);
             lds_barrier();
         }
     } else if (outw) {
         const int w = wave - 2;
-        half_t* out16 = reinterpret_cast<half_t*>(out);
-        // fp32 output: row of token t0 + 32 w of chunk ch, column pair * 32
         const size_t orow = (size_t)Hv * kD;
-        float* o32 = reinterpret_cast<float*>(out) + ((size_t)b * T + 32 * w) * orow + (size_t)h * kD + pair * 32;
+        // rows from this workgroup's first chunk on
+        half_t* out16 = reinterpret_cast<half_t*>(out) + (size_t)c0 * kC * orow;
+        // fp32 output: row of token t0 + 32 w of chunk ch, column pair * 32
+        float* o32 = reinterpret_cast<float*>(out) + ((size_t)b * T + c0 * kC + 32 * w) * orow + (size_t)h * kD +
+                     pair * 32;
         auto step = [&](int slot, int ch) {
             out_step<TIO>(sm.os[slot], sm.XS[slot], sm.OS[w], w, scale, o32 + (size_t)ch * kC * orow, orow,
-                          T - ch * kC - 32 * w);
+                          Tloc - ch * kC - 32 * w);
         };
         for (int it = 0; it <= nch; it += 2) {
-            if (!kF32 && it >= 2) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 2) * kC, pair, w);
-            if (it >= 1) step(1, it - 1);
+            if (outputs && !kF32 && it >= 2) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 2) * kC, pair, w, Tloc);
+            if (outputs && it >= 1) step(1, it - 1);
             lds_barrier();  // the O stores need not complete before the barrier
             if (it + 1 > nch) break;
-            if (!kF32 && it >= 1) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 1) * kC, pair, w);
-            step(0, it);
+            if (outputs && !kF32 && it >= 1) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 1) * kC, pair, w, Tloc);
+            if (outputs) step(0, it);
             lds_barrier();
         }
     } else {
@@ -971,20 +1044,22 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
         const unsigned rowbytes = kF32 ? (unsigned)kD * 2 : (unsigned)Hq * kD * 2;
         const size_t chunk_bytes = kF32 ? (size_t)kWsChunkF32 : (size_t)kC * rowbytes;
         const unsigned char* kh = kF32 ? wsh + kWsK
-                                       : reinterpret_cast<const unsigned char*>(k + ((size_t)b * T * Hq + hq) * kD);
+                                       : reinterpret_cast<const unsigned char*>(k + ((size_t)b * T * Hq + hq) * kD) +
+                                             (size_t)c0 * chunk_bytes;
         const unsigned char* qh = kF32 ? wsh + kWsQ
-                                       : reinterpret_cast<const unsigned char*>(q + ((size_t)b * T * Hq + hq) * kD);
+                                       : reinterpret_cast<const unsigned char*>(q + ((size_t)b * T * Hq + hq) * kD) +
+                                             (size_t)c0 * chunk_bytes;
         const unsigned slot_lds[4] = {(unsigned)(uintptr_t)(lds_void_t)(void*)&sm.cs[0],
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.cs[1],
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.os[0],
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.os[1]};
-        const unsigned* fl = flags + (size_t)bh * nch;
+        const unsigned* fl = flags + (size_t)bh * nch_all + c0;
         int* err = &sm.err[wave - 4];
         switch (wave) {
-            case 4: dma_role<0, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, T, nch); break;
-            case 5: dma_role<1, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, T, nch); break;
-            case 6: dma_role<2, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, T, nch); break;
-            default: dma_role<3, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, T, nch); break;
+            case 4: dma_role<0, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, Tloc, nch); break;
+            case 5: dma_role<1, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, Tloc, nch); break;
+            case 6: dma_role<2, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, Tloc, nch); break;
+            default: dma_role<3, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, Tloc, nch); break;
         }
     }
     if (chain) {
@@ -996,15 +1071,105 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
         if (mode == kCarryBeside && tid == 0 && lost)
             __hip_atomic_store(aborts + blockIdx.x, 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-        if (!(lost && mode == kCarryBeside)) {
+        // in order after the prep the abort words were not cleared: the first unit's
+        // workgroups zero theirs (a workgroup that runs in order never gives up)
+        if (mode == kCarryInOrder && tid == 0 && blockIdx.x < 4 * BHv)
+            __hip_atomic_store(aborts + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (dst && !(lost && mode == kCarryBeside)) {
             const float nan = __builtin_nanf("");
+            float* Dg = dst == state ? state + soff : dst + soff_seg;
 #pragma unroll
             for (int m = 0; m < 8; ++m)
-                *reinterpret_cast<float4*>(Sg + 16 * m + 4 * g) =
+                *reinterpret_cast<float4*>(Dg + 16 * m + 4 * g) =
                     lost ? make_float4(nan, nan, nan, nan) : make_float4(S[m][0], S[m][1], S[m][2], S[m][3]);
         }
-    } else if (outw && !kF32) {
-        out_flush(sm.OS[wave - 2], reinterpret_cast<half_t*>(out), b, T, Hv, h, (nch - 1) * kC, pair, wave - 2);
+    } else if (outw && outputs && !kF32) {
+        out_flush(sm.OS[wave - 2], reinterpret_cast<half_t*>(out) + (size_t)c0 * kC * Hv * kD, b, T, Hv, h,
+                  (nch - 1) * kC, pair, wave - 2, Tloc);
+    }
+}
+
+// The combine of the sequence split: entry[s + 1] = Phi_s entry[s] + Z_s for s = 1 .. nseg - 2,
+// in fp32.  Slots are stored [column][dk]; row j of the Phi slot is Phi's column j, so with
+// E = entry[s] stored the same way, entry[s + 1][c][d] = sum_j E[c][j] Phi[j][d] + Z[c][d].
+// State columns never mix: a workgroup takes R columns of one head through every step and
+// waits for no other workgroup.  Only the E chain is serial: wave w sums over j in
+// [32 w, 32 w + 32) with its lane's dk pair (2 lane, 2 lane + 1), holding that quarter of
+// Phi_s in registers while the next step's quarter loads; the four partial sums meet in LDS.
+// Every workgroup reads all of Phi_s per step whatever R is, while its FMA time grows with R:
+// the host picks the smallest R that keeps about one workgroup per CU.
+constexpr int kCombThreads = 256;
+template <int R>
+__global__ void __launch_bounds__(kCombThreads) gdn_seg_combine(float* __restrict__ seg, int nseg) {
+    const int bh = blockIdx.x / (kD / R), c0 = (blockIdx.x % (kD / R)) * R;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    float* segh = seg + (size_t)bh * nseg * kSegSlots * kSegSlotFloats;
+    auto slot = [&](int sg, int which) { return segh + ((size_t)sg * kSegSlots + which) * kSegSlotFloats; };
+    constexpr int kOut = (R * kD + kCombThreads - 1) / kCombThreads;  // outputs per thread
+    __shared__ __align__(16) float E[R][kD];
+    __shared__ __align__(16) float part[4][R][kD];
+    if (tid < R * kD / 4)
+        reinterpret_cast<float4*>(&E[0][0])[tid] =
+            reinterpret_cast<const float4*>(slot(1, kSegEntry) + (size_t)c0 * kD)[tid];
+    auto quarter = [&](int sg, float2 (&p)[32]) {
+        const float2* P = reinterpret_cast<const float2*>(slot(sg, kSegPhi) + (size_t)(32 * w) * kD) + lane;
+#pragma unroll
+        for (int jj = 0; jj < 32; ++jj) p[jj] = P[jj * (kD / 2)];
+    };
+    // this thread's outputs in the reduction: o = tid + 256 i < R * 128 is (row o / 128, dk o % 128)
+    auto zload = [&](int sg, float (&z)[kOut]) {
+        const float* Z = slot(sg, kSegZ) + (size_t)c0 * kD;
+#pragma unroll
+        for (int i = 0; i < kOut; ++i) z[i] = Z[min(tid + kCombThreads * i, R * kD - 1)];
+    };
+    // step sg computes with (pc, zc) while step sg + 1's quarter loads into (pn, zn); the loop
+    // is unrolled by two so the two register sets swap roles without copies
+    auto step = [&](int sg, const float2 (&pc)[32], const float (&zc)[kOut], float2 (&pn)[32], float (&zn)[kOut]) {
+        // unconditional (the last step reloads its own slot): a branch around the loads would
+        // make the compiler wait for them where the paths join
+        const int nx = min(sg + 1, nseg - 2);
+        quarter(nx, pn);
+        zload(nx, zn);
+        float2 acc[R] = {};
+#pragma unroll
+        for (int jj = 0; jj < 32; jj += 4) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float4 e = *reinterpret_cast<const float4*>(&E[r][32 * w + jj]);
+                acc[r].x = fmaf(e.x, pc[jj].x, acc[r].x);
+                acc[r].y = fmaf(e.x, pc[jj].y, acc[r].y);
+                acc[r].x = fmaf(e.y, pc[jj + 1].x, acc[r].x);
+                acc[r].y = fmaf(e.y, pc[jj + 1].y, acc[r].y);
+                acc[r].x = fmaf(e.z, pc[jj + 2].x, acc[r].x);
+                acc[r].y = fmaf(e.z, pc[jj + 2].y, acc[r].y);
+                acc[r].x = fmaf(e.w, pc[jj + 3].x, acc[r].x);
+                acc[r].y = fmaf(e.w, pc[jj + 3].y, acc[r].y);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) *reinterpret_cast<float2*>(&part[w][r][2 * lane]) = acc[r];
+        __syncthreads();  // partial sums written, E read by every wave
+        float* en = slot(sg + 1, kSegEntry) + (size_t)c0 * kD;
+#pragma unroll
+        for (int i = 0; i < kOut; ++i) {
+            const int o = tid + kCombThreads * i, r = o / kD, d = o % kD;
+            if (o < R * kD) {
+                const float v = zc[i] + part[0][r][d] + part[1][r][d] + part[2][r][d] + part[3][r][d];
+                E[r][d] = v;
+                en[o] = v;
+            }
+        }
+        __syncthreads();
+    };
+    float2 pa[32], pb[32];
+    float za[kOut], zb[kOut];
+    quarter(1, pa);
+    zload(1, za);
+    __syncthreads();
+    for (int sg = 1; sg + 1 < nseg; sg += 2) {
+        step(sg, pa, za, pb, zb);
+        if (sg + 2 >= nseg) break;
+        step(sg + 1, pb, zb, pa, za);
     }
 }
 
@@ -1014,13 +1179,63 @@ __global__ void __launch_bounds__(256) gdn_flags_clear(unsigned* __restrict__ w,
     if (i < n) w[i] = 0u;
 }
 
+// A positive integer from the environment, or `def` when unset or malformed.
+long env_long(const char* name, long def, long hi) {
+    const char* e = std::getenv(name);
+    if (!e || !*e) return def;
+    char* end = nullptr;
+    const long v = std::strtol(e, &end, 10);
+    return (end && *end == 0 && v >= 0 && v <= hi) ? v : def;
+}
+
+// The sequence split of a call: nseg segments of seg_len chunks (nseg == 1: no split).  It pays
+// where the carry's workgroups leave most CUs idle (few heads) and the chunk chain is long.
+// The call's serial time is about 2 (nch / nseg) chunk steps + (nseg - 2) combine steps (a
+// combine step costs about a chunk step), least near nseg = sqrt(2 nch); the plan takes the
+// most segments up to 1.5 sqrt(nch) whose maps launch ((2 nseg - 3) units of 4 workgroups per
+// head) fits in the 256 CUs of the part, each at least kMinSegChunks chunks long.  TSA_GDN_SEGMENTS
+// overrides the choice: 1 never splits, n >= 3 asks for n segments (fewer if the sequence has
+// fewer chunks).  The workspace size follows the plan, so a caller sizes the workspace with
+// the same setting it calls with (the entry points check the size they are given).
+constexpr int kSplitCUs = 256;
+constexpr int kMinSegChunks = 4;
+struct SegPlan {
+    int nseg = 1, seg_len = 0;
+};
+SegPlan seg_plan(int BHv, int nch) {
+    const long forced = env_long("TSA_GDN_SEGMENTS", 0, 1 << 20);
+    long n = 1;
+    if (forced >= 3)
+        n = std::min<long>(forced, nch);
+    else if (forced == 0 && BHv > 0)
+        n = std::min<long>(std::min<long>((kSplitCUs / (4 * BHv) + 3) / 2, nch / kMinSegChunks),
+                           (long)(1.5 * std::sqrt((double)nch)));
+    if (n < 3) return {};
+    const int seg_len = (int)((nch + n - 1) / n);
+    n = (nch + seg_len - 1) / seg_len;  // no empty segment
+    if (n < 3) return {};
+    return {(int)n, seg_len};
+}
+
+// Byte offset of the split's slots in the workspace: after the chunk workspaces, the ready
+// flags and the abort words, rounded up to 256 B.
+size_t seg_offset(size_t BHv, size_t nch, bool f32) {
+    const size_t end = BHv * nch * ((f32 ? kWsChunkF32 : kWsChunk) + sizeof(unsigned)) +
+                       BHv * (kD / (16 * kStrips)) * sizeof(unsigned);
+    return (end + 255) & ~(size_t)255;
+}
 }  // namespace
 
 size_t gdn_chunked_ws_bytes(int B, int T, int Hv, bool f32) {
     const size_t nch = (size_t)(T + kC - 1) / kC;
-    // chunk workspaces, then a ready flag per chunk, then an abort word per carry workgroup
-    return (size_t)B * Hv * nch * ((f32 ? kWsChunkF32 : kWsChunk) + sizeof(unsigned)) +
-           (size_t)B * Hv * (kD / (16 * kStrips)) * sizeof(unsigned);
+    const size_t BHv = (size_t)B * Hv;
+    // chunk workspaces, then a ready flag per chunk, then an abort word per carry workgroup,
+    // then the sequence split's entry / Z / Phi slots when the call splits
+    const SegPlan plan = seg_plan((int)BHv, (int)nch);
+    if (plan.nseg == 1)
+        return BHv * nch * ((f32 ? kWsChunkF32 : kWsChunk) + sizeof(unsigned)) +
+               BHv * (kD / (16 * kStrips)) * sizeof(unsigned);
+    return seg_offset(BHv, nch, f32) + BHv * plan.nseg * kSegSlots * kSegSlotFloats * sizeof(float);
 }
 
 namespace {
@@ -1039,15 +1254,6 @@ struct SideStream {
 constexpr int kMaxDevices = 64;
 std::mutex g_side_mu;
 SideStream g_side[kMaxDevices];
-
-// A positive integer from the environment, or `def` when unset or malformed.
-long env_long(const char* name, long def, long hi) {
-    const char* e = std::getenv(name);
-    if (!e || !*e) return def;
-    char* end = nullptr;
-    const long v = std::strtol(e, &end, 10);
-    return (end && *end == 0 && v >= 0 && v <= hi) ? v : def;
-}
 
 // Longest wait of a carry workgroup for a chunk, in ticks of the 100 MHz real-time counter.
 unsigned carry_wait_ticks() { return (unsigned)(env_long("TSA_GDN_CARRY_WAIT_US", 2000, 10000000) * 100); }
@@ -1082,12 +1288,35 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
                            nch, BHv);
         return hipGetLastError();
     };
-    auto carry = [&](int mode, unsigned ticks) {
-        hipLaunchKernelGGL(gdn_chunk_carry<TIO>, dim3(carry_wgs), dim3(kCarryThreads), 0, stream, Q, K, W,
-                           flags, aborts, mode, ticks, state, static_cast<TIO*>(out), T, Hq, Hv,
-                           nch, BHv, scale);
+    auto carry = [&](int mode, unsigned ticks, int units = 1, CarryJob job = CarryJob{}) {
+        hipLaunchKernelGGL(gdn_chunk_carry<TIO>, dim3(units * carry_wgs), dim3(kCarryThreads), 0, stream, Q, K,
+                           W, flags, aborts, mode, ticks, state, static_cast<TIO*>(out), T, Hq, Hv, nch, BHv,
+                           scale, job);
         return hipGetLastError();
     };
+
+    // Sequence split: in order on the caller's stream (the maps need every chunk's operands)
+    const SegPlan plan = seg_plan(BHv, nch);
+    if (plan.nseg > 1) {
+        CarryJob job;
+        job.phase = kJobMaps;
+        job.nseg = plan.nseg;
+        job.seg_len = plan.seg_len;
+        job.seg = reinterpret_cast<float*>(W + seg_offset(BHv, nch, std::is_same<TIO, float>::value));
+        hipError_t e = prep(stream);
+        if (e == hipSuccess) e = carry(kCarryInOrder, wait_ticks, 2 * plan.nseg - 3, job);
+        if (e == hipSuccess) {
+            // state columns per combine workgroup: about one workgroup per CU
+            const int rows = BHv <= 2 ? 1 : BHv <= 4 ? 2 : BHv <= 8 ? 4 : 8;
+            auto combine = rows == 1 ? gdn_seg_combine<1> : rows == 2 ? gdn_seg_combine<2>
+                         : rows == 4 ? gdn_seg_combine<4> : gdn_seg_combine<8>;
+            hipLaunchKernelGGL(combine, dim3(BHv * (kD / rows)), dim3(kCombThreads), 0, stream, job.seg, plan.nseg);
+            e = hipGetLastError();
+        }
+        job.phase = kJobFinish;
+        if (e == hipSuccess) e = carry(kCarryInOrder, wait_ticks, plan.nseg - 1, job);
+        return e;
+    }
 
     // Overlap only when it cannot stall: the carry's workgroups (one per CU) must leave at
     // least half the CUs to the prep, and a stream being captured into a graph runs the two
@@ -1116,12 +1345,12 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
         }
         if (d.ok && 2 * carry_wgs <= d.cus) side = &d;
     }
-    hipError_t e = clear();
-    if (e != hipSuccess) return e;
-    if (!side) {
-        e = prep(stream);
+    if (!side) {  // in order: no flag clear needed
+        const hipError_t e = prep(stream);
         return e != hipSuccess ? e : carry(kCarryInOrder, wait_ticks);
     }
+    hipError_t e = clear();
+    if (e != hipSuccess) return e;
     // fork: the prep starts after the caller's earlier work (the flag clear included); the
     // carry is queued first so its workgroups take their CUs before the prep fills the rest.
     // join: the caller's stream waits for the prep, then the second carry launch redoes any
@@ -1146,9 +1375,10 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
 // passes the array's name to a kernel (on the host it is only a stand-in for the symbol):
 // the device address comes from hipGetSymbolAddress, once per device, on the first call on
 // that device, and is kept in g_scratch.  Every call on a GPU shares that GPU's array and
-// leaves its contents behind; the ready flags and abort words that must start at zero are
-// cleared by the call's first kernel (the rest of the workspace is written before it is
-// read).  Calls that overlap on one GPU race on the array.
+// leaves its contents behind: the call runs the prep and the carry in order, so the ready
+// flags it reads are set by its own prep, the carry zeroes the abort words, and the rest of
+// the workspace is written before it is read.  Calls that overlap on one GPU race on the
+// array.
 constexpr size_t kScratchBytes = 64ull << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
