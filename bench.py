@@ -28,7 +28,9 @@ reference's target model (B=1, 24 query / 4 K/V heads, D=256, S=8192, causal, ga
 softmax) is timed on its own and reported as the part `attn_gqa_gated`; so is the GDN
 recurrence with the layer's pre/post ops at the prefill shape (`gdn_layer_ops`): raw q/k
 and gate projections -> fused chunked prefill -> gated RMSNorm, against the unfused
-pipeline (pre-op pass, chunked prefill, gated RMSNorm); and, for context only, the GDN
+pipeline (pre-op pass, chunked prefill, gated RMSNorm); and, for context only, one GPU's
+share of the prefill under 8-way head sharding (2 QK / 4 V heads, `gdn_prefill_head_shard`:
+the call splits the sequence, timed beside the same call without the split) and the GDN
 layer at the reference's own published shape (T=512, 16 QK / 48 V heads, its LCG inputs:
 token-serial and chunked, `gdn_reference_shape`) beside its 2080 Ti times.
 Last (skip with --no-sustained), the attention kernel runs back to back for ~6 s with the
@@ -533,6 +535,43 @@ def main():
     unfused_ms = time_fn(unfused_layer, n_lay)
     rms_ms = time_fn(rms_only, n_lay)
 
+    # context: one GPU's share of the prefill under 8-way head sharding (Hq=2, Hv=4 of the
+    # 16 / 32 heads).  With so few heads the chunk carry alone would leave most CUs idle, so
+    # the call splits the sequence (segment transition maps side by side, then a combine);
+    # the same call with the split turned off (TSA_GDN_SEGMENTS=1) is timed beside it.
+    shq, shv = PREFILL["Hq"] // 8, PREFILL["Hv"] // 8
+    sq, sk = (x[:, :, :shq].contiguous() for x in (pre["q"], pre["k"]))
+    sv = pre["v"][:, :, :shv].contiguous()
+    sg, sb = (x[:, :, :shv].contiguous() for x in (pre["g"], pre["beta"]))
+    sst = torch.zeros(PREFILL["B"], shv, PREFILL["d"], PREFILL["d"], device=dev)
+    so = torch.empty_like(sv)
+
+    def shard_ms(segments):
+        old = os.environ.pop("TSA_GDN_SEGMENTS", None)
+        if segments is not None:
+            os.environ["TSA_GDN_SEGMENTS"] = segments
+        try:
+            nbytes = tsa.gdn_chunked_workspace_bytes(PREFILL["B"], PREFILL["T"], shq, shv)
+            sws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+            def f():
+                sst.zero_()
+                tsa.gdn_chunked_fwd(sq, sk, sv, sg, sb, sst, so, ws=sws, stream=stream)
+            return time_fn(f, n_lay), nbytes
+        finally:
+            os.environ.pop("TSA_GDN_SEGMENTS", None)
+            if old is not None:
+                os.environ["TSA_GDN_SEGMENTS"] = old
+
+    def shard_zero():
+        sst.zero_()
+
+    shard_zero_ms = time_fn(shard_zero, n_lay)
+    shard_split_ms, shard_ws = shard_ms(None)
+    shard_plain_ms, shard_ws_plain = shard_ms("1")
+    shard_split_ms -= shard_zero_ms
+    shard_plain_ms -= shard_zero_ms
+
     # context: one GDN layer at the reference's published shape (T=512, Hq=16, Hv=48), fp32
     # q / k / v / out as the reference's kernels take them (src/gdn_sm75.cu:57-64), inputs in
     # the ranges of its LCG generator (:1270-1279), state from zero
@@ -581,7 +620,8 @@ def main():
 
     finite = bool(torch.isfinite(a["o"]).all() and torch.isfinite(pre["out"]).all()
                   and torch.isfinite(pre["state"]).all() and torch.isfinite(dec["out"]).all()
-                  and torch.isfinite(gq["o"]).all() and torch.isfinite(lay["y"]).all())
+                  and torch.isfinite(gq["o"]).all() and torch.isfinite(lay["y"]).all()
+                  and torch.isfinite(so).all() and torch.isfinite(sst).all())
 
     traffic = load_traffic()
     fa = attn_flops(**ATTN)
@@ -613,6 +653,16 @@ def main():
             "roofline": roof("mfma", pre_tflops, PEAK_MFMA_F16_TFLOPS, "TFLOP/s", "gdn_prefill"),
             "hbm_frac": round(bp / (ms["gdn_prefill"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "carry_workgroups_redone_last_call": redo,
+        },
+        "gdn_prefill_head_shard": {
+            "workload": "context only: one GPU's share of the chunked GDN prefill under 8-way "
+                        f"head sharding, B=1 T={PREFILL['T']} Hq={shq} Hv={shv} d=128 C=64, fp16 "
+                        "I/O, state from zero; timed outside the step",
+            "ms_sequence_split": round(shard_split_ms, 5), "ms_no_split": round(shard_plain_ms, 5),
+            "tok_s": round(PREFILL["B"] * PREFILL["T"] / (shard_split_ms * 1e-3), 1),
+            "mfma_frac": round(prefill_flops(**dict(PREFILL, Hq=shq, Hv=shv)) / (shard_split_ms * 1e-3)
+                               / 1e12 / PEAK_MFMA_F16_TFLOPS, 4),
+            "workspace_bytes": shard_ws, "workspace_bytes_no_split": shard_ws_plain,
         },
         "gdn_reference_shape": {
             "workload": "context only: one GDN layer at the reference's published shape, B=1 "
