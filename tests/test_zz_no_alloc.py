@@ -1,7 +1,8 @@
 """tsa_gdn_chunked_fwd_noalloc, the chunked prefill on the library's fixed device scratch
 array instead of a caller workspace, called through the C-ABI and checked against
 tsa_gdn_chunked_fwd (the same kernels, so bit for bit) on two calls in a row, the second
-smaller than the first, and on the largest shape the 64 MiB scratch holds."""
+smaller than the first, on the largest shape the 64 MiB scratch holds, and on shapes where
+the call splits the sequence."""
 import ctypes
 import math
 
@@ -54,3 +55,16 @@ def test_noalloc_largest_shape(dev):
     assert tsa.gdn_chunked_workspace_bytes(1, 2240, 16, 32) <= 64 << 20
     _case(dev, 13, 1, 2240, 16, 32)
     _case(dev, 14, 1, 70, 2, 3)
+
+
+def test_noalloc_sequence_split(dev, monkeypatch):
+    """Few heads and many chunks: the call splits the sequence (its Phi / Z / entry slots in
+    the scratch too), on two calls in a row, the second smaller."""
+    monkeypatch.delenv("TSA_GDN_SEGMENTS", raising=False)
+    for B, T, Hq, Hv in ((1, 2048, 2, 4), (1, 1000, 1, 2)):
+        split = tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv)
+        monkeypatch.setenv("TSA_GDN_SEGMENTS", "1")
+        assert split > tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv)
+        monkeypatch.delenv("TSA_GDN_SEGMENTS")
+    _case(dev, 15, 1, 2048, 2, 4)
+    _case(dev, 16, 1, 1000, 1, 2)
