@@ -51,7 +51,7 @@ def _direct(dev, q, k, v, g, beta, st, f32=False):
     return o.cpu(), ts.cpu()
 
 
-@pytest.mark.parametrize("T", [1, 20, 31, 32, 300])
+@pytest.mark.parametrize("T", [1, 20, 31, 32, 300, 1500])  # 1500: 2 x 6 heads, the sequence split
 def test_dense_fp16_in_place(dev, T):
     import torch
     B, Hk, Hv = 2, 2, 6
