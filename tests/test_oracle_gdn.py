@@ -21,7 +21,8 @@ instead of 1).  The build pins chunked GDN to the serial recurrence, never to th
 Pins: float64 matrix-form fixtures (tests/golden/gdn_golden.npz); closed forms (beta = 0,
 one token from a zero state, the delta rule's exact write of v under key k, orthonormal
 keys); chunked(f64, exact) == serial for C = 16/32/64 and ragged T; the C = 2 closed form of
-the reference's solve; prefill/decode state continuity; a planted head-map mistake.
+the reference's solve; prefill/decode state continuity; the affine segment map the
+sequence split composes; a planted head-map mistake.
 """
 import numpy as np
 import pytest
@@ -181,6 +182,27 @@ def test_prefill_then_decode_equals_serial(orc):
     o2, s2 = orc.gdn_serial(q[:, 69:], k[:, 69:], v[:, 69:], g[:, 69:], beta[:, 69:], s1)
     assert _rel(s2, s_all) < 1e-5
     assert np.abs(o2[:, 0] - o_all[:, 69]).max() < 1e-5
+
+
+def test_segment_state_map_is_affine(orc):
+    """The premise of the chunked prefill's sequence split: over a segment the state update is
+    affine in the entering state, S_out = Phi S_in + Z, where Z is the segment run from a zero
+    state and Phi the segment run with v = 0 from the identity.  With the state stored
+    [dv][dk] that reads st_out = st_in @ st_Phi + st_Z (the combine's E' = E P + Z).  A slow
+    gate keeps Phi far from both zero and the identity; the transposed composition fails."""
+    rng = np.random.default_rng(23)
+    B, T, Hq, Hv = 1, 150, 1, 2
+    q, k, v, g, beta, _ = _inputs(rng, B, T, Hq, Hv)
+    g = (-0.01 * (1 + 0.5 * rng.standard_normal(g.shape))).astype(np.float32)
+    s_in = (0.5 * rng.standard_normal((B, Hv, D, D))).astype(np.float32)
+    eye = np.broadcast_to(np.eye(D, dtype=np.float32), (B, Hv, D, D)).copy()
+    _, s_out = orc.gdn_serial(q, k, v, g, beta, s_in)
+    _, z = orc.gdn_serial(q, k, v, g, beta, np.zeros_like(s_in))
+    _, phi = orc.gdn_serial(q, k, np.zeros_like(v), g, beta, eye)
+    s64, p64 = s_in.astype(np.float64), phi.astype(np.float64)
+    assert _rel(np.einsum("bhjd,bhde->bhje", s64, p64) + z, s_out) < 1e-5
+    assert np.abs(phi - eye).max() > 0.05 and np.abs(phi).max() > 0.1
+    assert _rel(np.einsum("bhjd,bhed->bhje", s64, p64) + z, s_out) > 1e-2
 
 
 def test_serial_thread_count_does_not_change_results(orc):
