@@ -94,8 +94,13 @@ int tsa_attn_gqa_naive(const void* q, const void* k, const void* v, const void* 
  * :271-292, is only first-order accurate).  dk = dv = 128, chunk = 64.  ws must hold
  * tsa_gdn_chunked_workspace_bytes(...) bytes of device memory, the caller's as the
  * reference driver owns the two-pass scratch (src/gdn_sm75.cu:1341-1346); its contents on
- * entry do not matter (each call clears its own ready flags first), and calls that share
- * one ws must be ordered on one stream. */
+ * entry do not matter (a call whose two kernels run side by side clears its ready flags
+ * first; one that runs them in order needs no clear), and calls that share one ws must be
+ * ordered on one stream.  With few heads and many chunks (B*Hv <= 21, at least 12 chunks)
+ * the call splits the sequence into segments (segment state maps side by side, then a
+ * combine) and the workspace grows by 192 KiB per head and segment; the environment
+ * variable TSA_GDN_SEGMENTS, read by both functions, overrides that plan (1: never split,
+ * n >= 3: n segments), so a caller sizes ws under the setting it calls with. */
 size_t tsa_gdn_chunked_workspace_bytes(int B, int T, int Hq, int Hv, int dk, int dv,
                                        int chunk);
 int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v, const float* g_log,
@@ -121,7 +126,7 @@ int tsa_gdn_chunked_fwd_f32(const float* q, const float* k, const float* v, cons
  * itself (src/gdn_sm75.cu:1341-1346).  The workspace is a fixed 64 MiB device array inside
  * the library, one per GPU, held until the process ends; shapes whose
  * tsa_gdn_chunked_workspace_bytes(...) exceed 64 MiB return TSA_ERR_SCRATCH (e.g. 32 V-heads
- * up to T = 2240).  Nothing is allocated, no stream or event is created (the two kernels run
+ * up to T = 2240).  Nothing is allocated, no stream or event is created (the kernels run
  * in order on `stream`), and the results equal tsa_gdn_chunked_fwd's.  Every call on a GPU
  * uses that GPU's one array: calls that overlap on one GPU (other streams, other host
  * threads) race and must be ordered by the caller. */
