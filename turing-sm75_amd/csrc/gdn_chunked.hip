@@ -957,7 +957,8 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
     float us = 1.f;
     const float* src = state;
     float* dst = state;
-    float* segh = job.seg + (size_t)bh * job.nseg * kSegSlots * kSegSlotFloats;  // this head's slots
+    // this head's slots (no slots in the plain job)
+    float* segh = job.seg ? job.seg + (size_t)bh * job.nseg * kSegSlots * kSegSlotFloats : nullptr;
     auto slot = [&](int sg, int which) { return segh + ((size_t)sg * kSegSlots + which) * kSegSlotFloats; };
     if (job.phase == kJobMaps) {
         if (unit == 0) {            // segment 0 from the caller's state; its end enters segment 1
