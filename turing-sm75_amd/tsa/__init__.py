@@ -250,6 +250,9 @@ def _gdn_shapes(q, k, v, g_log, beta, state, batched_t: bool):
 
 
 def gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk=128, dv=128, chunk=64, f32=False) -> int:
+    """Workspace bytes of one chunked call.  With few heads and many chunks the call splits the
+    sequence and needs more (TSA_GDN_SEGMENTS, read at each query and call, overrides the
+    plan: query under the setting the call will see)."""
     fn = load().tsa_gdn_chunked_workspace_bytes_f32 if f32 else load().tsa_gdn_chunked_workspace_bytes
     return int(fn(B, T, Hq, Hv, dk, dv, chunk))
 
@@ -257,7 +260,9 @@ def gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk=128, dv=128, chunk=64, f32=Fals
 def gdn_chunked_fwd(q, k, v, g_log, beta, state, out=None, scale=None, chunk=64, ws=None,
                     stream=None):
     """Chunked prefill; state [B, Hv, dv, dk] is updated in place; returns out.  fp32 q/k/v
-    select tsa_gdn_chunked_fwd_f32 (fp32 out)."""
+    select tsa_gdn_chunked_fwd_f32 (fp32 out).  With few heads (B*Hv <= 21) and at least 12
+    chunks the library splits the sequence into segments run side by side (same results to
+    fp32 rounding)."""
     import torch
     B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, True)
     out = _out(out, v)
