@@ -457,3 +457,50 @@ def test_chunked_under_serialised_dispatch(dev):
                        env=env, capture_output=True, text=True, timeout=240)
     print(r.stdout[-2000:], r.stderr[-2000:])
     assert r.returncode == 0
+
+
+@pytest.mark.parametrize("shape", [(1, 1000, 4, 8), (1, 2048, 2, 4)], ids=["plain", "split"])
+def test_chunked_under_graph_capture(dev, monkeypatch, shape):
+    """Captured into a HIP graph, a chunked call runs its kernels in order on the capturing
+    stream (no side stream, no memset node); each of three replays, with eager work and
+    synchronisations between them, reproduces the eager call bit for bit -- on a plain shape
+    and on one that splits the sequence, through tsa_gdn_chunked_fwd and the no-allocation
+    entry point."""
+    import ctypes
+    import torch
+    monkeypatch.delenv("TSA_GDN_SEGMENTS", raising=False)
+    B, T, Hq, Hv = shape
+    print(f"graph capture B={B} T={T} Hq={Hq} Hv={Hv}", flush=True)
+    rng = np.random.default_rng(T + Hv)
+    q, k, v, g, beta, st0 = _dev(dev, *_inputs(rng, B, T, Hq, Hv, sstd=0.02))
+    ws = torch.empty(tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv), dtype=torch.uint8, device=dev)
+    lib = tsa.load()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    scale = 1.0 / np.sqrt(D)
+
+    def call(ts, out, stream, noalloc):
+        if noalloc:
+            rc = lib.tsa_gdn_chunked_fwd_noalloc(p(q), p(k), p(v), p(g), p(beta), p(ts), p(out), B, T, Hq,
+                                                 Hv, D, D, 64, scale, ctypes.c_void_p(stream.cuda_stream))
+            assert rc == tsa.TSA_OK, tsa.strerror(rc)
+        else:
+            tsa.gdn_chunked_fwd(q, k, v, g, beta, ts, out, ws=ws, stream=stream)
+
+    for noalloc in (False, True):
+        ts, out = st0.clone(), torch.empty_like(v)
+        call(ts, out, torch.cuda.current_stream(), noalloc)  # eager (also sets the scratch up)
+        torch.cuda.synchronize()
+        o_ref, s_ref = out.clone(), ts.clone()
+        side = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        ts.copy_(st0)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            call(ts, out, side, noalloc)
+        for _ in range(3):
+            ts.copy_(st0)
+            out.fill_(7.0)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, o_ref) and torch.equal(ts, s_ref), f"noalloc={noalloc}"
