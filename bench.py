@@ -537,7 +537,7 @@ def main():
 
     # context: one GPU's share of the prefill under 8-way head sharding (Hq=2, Hv=4 of the
     # 16 / 32 heads).  With so few heads the chunk carry alone would leave most CUs idle, so
-    # the call splits the sequence (segment transition maps side by side, then a combine);
+    # the call splits the sequence (segment state maps side by side, a combine, a fix-up);
     # the same call with the split turned off (TSA_GDN_SEGMENTS=1) is timed beside it.
     shq, shv = PREFILL["Hq"] // 8, PREFILL["Hv"] // 8
     sq, sk = (x[:, :, :shq].contiguous() for x in (pre["q"], pre["k"]))

@@ -96,11 +96,12 @@ int tsa_attn_gqa_naive(const void* q, const void* k, const void* v, const void* 
  * reference driver owns the two-pass scratch (src/gdn_sm75.cu:1341-1346); its contents on
  * entry do not matter (a call whose two kernels run side by side clears its ready flags
  * first; one that runs them in order needs no clear), and calls that share one ws must be
- * ordered on one stream.  With few heads and many chunks (B*Hv <= 21, at least 12 chunks)
- * the call splits the sequence into segments (segment state maps side by side, then a
- * combine) and the workspace grows by 192 KiB per head and segment; the environment
- * variable TSA_GDN_SEGMENTS, read by both functions, overrides that plan (1: never split,
- * n >= 3: n segments), so a caller sizes ws under the setting it calls with. */
+ * ordered on one stream.  With few heads and many chunks (B*Hv <= 21, at least 16 chunks)
+ * the call splits the sequence into segments (segment state maps with their outputs side by
+ * side, a combine, a parallel output fix-up) and the workspace grows by 192 KiB per head and
+ * segment and 1 KiB per head and token after the first segment; the environment variable
+ * TSA_GDN_SEGMENTS, read by both functions, overrides that plan (1: never split, n >= 2:
+ * n segments), so a caller sizes ws under the setting it calls with. */
 size_t tsa_gdn_chunked_workspace_bytes(int B, int T, int Hq, int Hv, int dk, int dv,
                                        int chunk);
 int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v, const float* g_log,

@@ -131,36 +131,40 @@ def test_gdn_workspace_bytes_scales_with_chunks():
 
 def test_gdn_workspace_bytes_with_sequence_split(monkeypatch):
     # few heads and many chunks split the sequence: after the flags and abort words, at a
-    # 256-byte boundary, three 64 KiB fp32 slots (entry state, Z, Phi) per head and segment
+    # 256-byte boundary, three 64 KiB fp32 slots (entry state, Z, Phi) per head and segment,
+    # then per head two fp32 rows of 128 (the maps' O_Z and M) per token after segment 0
     monkeypatch.delenv("TSA_GDN_SEGMENTS", raising=False)
     base = lambda BHv, nch: BHv * (nch * (58368 + 4) + 4 * 4)
-    split = lambda BHv, nch, nseg: (base(BHv, nch) + 255) // 256 * 256 + BHv * nseg * 3 * 65536
-    # 4 heads, 64 chunks: 8 segments of 8 chunks (the maps launch, 13 units x 4 workgroups x
-    # 4 heads, fits 256 CUs; 9 segments of 8, 8, ..., 0 would leave one empty)
-    assert tsa.gdn_chunked_workspace_bytes(1, 4096, 2, 4) == split(4, 64, 8)
-    # 1 head, 64 chunks: at most 1.5 sqrt(64) = 12 segments, so 6 chunks each, which takes 11
-    # segments (the last of 4 chunks); 256 chunks: 24 segments of 11 chunks (the last of 3)
-    assert tsa.gdn_chunked_workspace_bytes(1, 4096, 1, 1) == split(1, 64, 11)
-    assert tsa.gdn_chunked_workspace_bytes(1, 16384, 1, 1) == split(1, 256, 24)
-    # 16 chunks: at least 4 chunks a segment
-    assert tsa.gdn_chunked_workspace_bytes(1, 1024, 1, 1) == split(1, 16, 4)
-    # 32 heads: the carry already takes half the CUs, no split; 11 chunks: too short to split
+    rows = lambda BHv, T, L: 2 * BHv * (T - 64 * L) * 512
+    split = lambda BHv, nch, nseg, T, L: ((base(BHv, nch) + 255) // 256 * 256 + BHv * nseg * 3 * 65536 +
+                                           rows(BHv, T, L))
+    # 4 heads, 64 chunks: 8 segments of 8 chunks (the maps launch, 15 units x 4 workgroups x
+    # 4 heads, fits 256 CUs; sqrt(64) = 8)
+    assert tsa.gdn_chunked_workspace_bytes(1, 4096, 2, 4) == split(4, 64, 8, 4096, 8)
+    # 1 head: 8 segments at 64 chunks, 16 of 16 chunks at 256, 2 of 8 at 16 (8 chunks at least)
+    assert tsa.gdn_chunked_workspace_bytes(1, 4096, 1, 1) == split(1, 64, 8, 4096, 8)
+    assert tsa.gdn_chunked_workspace_bytes(1, 16384, 1, 1) == split(1, 256, 16, 16384, 16)
+    assert tsa.gdn_chunked_workspace_bytes(1, 1024, 1, 1) == split(1, 16, 2, 1024, 8)
+    # 16 heads: 2 segments (3 units x 64 workgroups); 32 heads: the carry already takes half
+    # the CUs, no split; 11 chunks: too short to split
+    assert tsa.gdn_chunked_workspace_bytes(1, 4096, 8, 16) == split(16, 64, 2, 4096, 32)
     assert tsa.gdn_chunked_workspace_bytes(1, 4096, 16, 32) == base(32, 64)
     assert tsa.gdn_chunked_workspace_bytes(1, 704, 2, 4) == base(4, 11)
     monkeypatch.setenv("TSA_GDN_SEGMENTS", "1")
     assert tsa.gdn_chunked_workspace_bytes(1, 4096, 2, 4) == base(4, 64)
     monkeypatch.setenv("TSA_GDN_SEGMENTS", "3")
-    assert tsa.gdn_chunked_workspace_bytes(1, 1000, 1, 2) == split(2, 16, 3)  # 6 + 6 + 4
-    assert tsa.gdn_chunked_workspace_bytes(1, 128, 1, 2) == base(2, 2)  # 2 chunks: no split
+    assert tsa.gdn_chunked_workspace_bytes(1, 1000, 1, 2) == split(2, 16, 3, 1000, 6)  # 6 + 6 + 4
+    assert tsa.gdn_chunked_workspace_bytes(1, 128, 1, 2) == split(2, 2, 2, 128, 1)  # 2 chunks: 2 of 1
+    assert tsa.gdn_chunked_workspace_bytes(1, 64, 1, 2) == base(2, 1)  # 1 chunk: no split
     monkeypatch.setenv("TSA_GDN_SEGMENTS", "5")
-    assert tsa.gdn_chunked_workspace_bytes(2, 777, 3, 4) == split(8, 13, 5)  # 3 x 4 + 1
+    assert tsa.gdn_chunked_workspace_bytes(2, 777, 3, 4) == split(8, 13, 5, 777, 3)  # 3 x 4 + 1
     monkeypatch.setenv("TSA_GDN_SEGMENTS", "1000")
-    assert tsa.gdn_chunked_workspace_bytes(2, 777, 3, 4) == split(8, 13, 13)  # one chunk each
+    assert tsa.gdn_chunked_workspace_bytes(2, 777, 3, 4) == split(8, 13, 13, 777, 1)  # one chunk each
     monkeypatch.setenv("TSA_GDN_SEGMENTS", "4")
     # fp32 I/O: the chunk workspace also holds the fp16 K / Q rows
     f32base = 4 * (18 * (58368 + 32768 + 4) + 4 * 4)
     assert tsa.gdn_chunked_workspace_bytes(1, 1100, 2, 4, f32=True) == \
-        (f32base + 255) // 256 * 256 + 4 * 4 * 3 * 65536
+        (f32base + 255) // 256 * 256 + 4 * 4 * 3 * 65536 + rows(4, 1100, 5)
 
 
 def test_gdn_noalloc_argument_errors():

@@ -169,13 +169,16 @@ def test_ragged_and_head_map(dev, orc, kind, T):
     _check(o, s, o_ref, s_ref, *TOL[kind], label=f"{kind} T={T}")
 
 
-# The sequence split (few heads, many chunks): segments' transition maps run side by side and
-# are combined (state after a segment = Phi state before + Z) before the segments' outputs.
+# The sequence split (few heads, many chunks): segments' transition maps run side by side with
+# their outputs, are combined (state after a segment = Phi state before + Z), and each chunk's
+# output is then fixed up in parallel (O = O_Z + M E).
 # TSA_GDN_SEGMENTS: None = the library's choice, "1" = no split, n = n segments.
 SPLIT_CASES = [
-    (1, 4096, 2, 4, None),  # 8 segments of 8 chunks (the library's choice for 4 heads)
-    (1, 1000, 1, 2, "3"),   # 6 + 6 + 4 chunks, the last chunk 40 tokens
-    (2, 777, 3, 4, "5"),    # 3 + 3 + 3 + 3 + 1 chunks, Hv % Hq != 0
+    (1, 4096, 2, 4, None),   # 8 segments of 8 chunks (the library's choice for 4 heads)
+    (1, 2048, 8, 16, None),  # 16 heads: 2 segments of 16 chunks
+    (1, 1000, 1, 2, "3"),    # 6 + 6 + 4 chunks, the last chunk 40 tokens
+    (2, 777, 3, 4, "5"),     # 3 + 3 + 3 + 3 + 1 chunks, Hv % Hq != 0
+    (1, 200, 1, 2, "2"),     # 2 + 2 chunks, the last one 8 tokens
 ]
 
 
@@ -215,7 +218,7 @@ def test_sequence_split(dev, orc, monkeypatch, case, decay):
 
 def test_sequence_split_fp32_io(dev, orc, monkeypatch):
     """The split with fp32 I/O (K / Q rows from the prep's fp16 copies in the workspace):
-    4 segments of 5, 5, 5 and 3 chunks."""
+    2 segments of 9 chunks."""
     rng = np.random.default_rng(411)
     B, T, Hq, Hv = 1, 1100, 2, 4
     q, k, v, g, beta, st = (a.astype(np.float32) for a in _inputs(rng, B, T, Hq, Hv, sstd=0.02))

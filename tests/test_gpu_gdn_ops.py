@@ -106,8 +106,8 @@ CASES = [  # B, T, Hq, Hv
     (2, 130, 2, 6),      # batch, ragged
     (1, 1, 1, 1),
     (1, 4096, 16, 32),   # the T=4096, Hq=16, Hv=32 prefill from raw inputs
-    (1, 2048, 2, 4),     # few heads, 32 chunks: the call splits the sequence (8 segments)
-    (1, 1500, 1, 3),     # split into 6 segments of 4 chunks, the last chunk ragged
+    (1, 2048, 2, 4),     # few heads, 32 chunks: the call splits the sequence (4 segments)
+    (1, 1500, 1, 3),     # split into 3 segments of 8 chunks, the last chunk ragged
 ]
 
 

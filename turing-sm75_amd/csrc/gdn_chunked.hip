@@ -90,23 +90,32 @@ constexpr int kCarryBeside = 1;   // beside the prep: a timed-out workgroup abor
 constexpr int kCarryRetry = 2;    // after the prep: only the first launch's aborted workgroups run
 
 // Sequence split (few heads, many chunks): T is cut into nseg segments of seg_len chunks (the
-// last takes the rest).  The state after a segment is an affine map of the state before it,
-// S_out = Phi S_in + Z, where Z is the segment's chain run from S = 0 and Phi its chain run
-// from S = I with U = 0 (the state update is linear in S and in U).  Three launches:
-//   maps   -- segment 0's chain from the caller's state (its outputs, and its end state as
-//             segment 1's entry), and, side by side, Z and Phi of segments 1 .. nseg-2;
-//   combine (gdn_seg_combine) -- entry[s+1] = Phi_s entry[s] + Z_s, s = 1 .. nseg-2;
-//   finish -- segments 1 .. nseg-1 from their entry states, with outputs; the last one's end
-//             state is the call's result.
-// The serial depth drops from nch chunk steps to about 2 seg_len + the combine.  Per (b, h,
-// segment) the workspace holds three [128 columns][128] fp32 slots: entry, Z, Phi.
-constexpr int kJobPlain = 0, kJobMaps = 1, kJobFinish = 2;
+// last takes the rest).  The state update is linear in the state and in U, so the state
+// after a segment is an affine map of the state E entering it, S_out = Phi E + Z, where Z is
+// the segment's chain run from S = 0 and Phi its chain run from S = I with U = 0; and a
+// chunk's output, O = A S + B, is then O = O_Z + M E, where O_Z is the output of the Z chain
+// and M = A Phi_<c the output of the Phi chain (U = 0 makes B vanish).  Three launches after
+// the prep:
+//   maps    -- segment 0's chain from the caller's state (its outputs, and its end state as
+//              segment 1's entry), and, side by side, the Z and Phi chains of segments
+//              1 .. nseg-1 with their outputs O_Z and M (fp32, to the workspace);
+//   combine (gdn_seg_combine) -- E[s+1] = Phi_s E[s] + Z_s for s = 1 .. nseg-1, the last
+//              one the call's final state;
+//   fixup   (gdn_seg_fixup) -- O = O_Z + M E for every chunk of segments 1 .. nseg-1, all
+//              chunks in parallel.
+// The serial depth drops from nch chunk steps to seg_len chunk steps + nseg - 1 combine
+// steps.  Per (b, h, segment) the workspace holds three [128 columns][128] fp32 slots
+// (entry E, Z, Phi), and per (b, h) the O_Z and M rows of the tokens after segment 0.
+constexpr int kJobPlain = 0, kJobMaps = 1;
 constexpr int kSegSlots = 3, kSegEntry = 0, kSegZ = 1, kSegPhi = 2;
 constexpr size_t kSegSlotFloats = (size_t)kD * kD;
 struct CarryJob {
     int phase = kJobPlain;
     int nseg = 1, seg_len = 0;
+    int Tr = 0;            // tokens after segment 0: rows of oz / om per (b, h)
     float* seg = nullptr;  // [B*Hv][nseg][kSegSlots][kD][kD]
+    float* oz = nullptr;   // [B*Hv][Tr][kD]: O_Z, the Z chains' outputs
+    float* om = nullptr;   // [B*Hv][Tr][kD]: M, the Phi chains' outputs
 };
 
 // Within each aligned 32-block, index 16a + 4g + b is stored at 8g + 4a + b.  A 16x16x32
@@ -950,13 +959,14 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
     const int sl = wave & 1;  // chain wave: its strip; output wave: w = wave - 2
 
     // This workgroup's chunks [c0, c0 + nch), where its state starts (src: loaded; else zero,
-    // or the identity for a transition map), where it ends (dst, or nowhere), whether it
-    // stores outputs, and the U scale (0 for a transition map).
+    // or the identity for a transition map), where it ends (dst), where its outputs go (out,
+    // or a map's fp32 rows in the workspace), and the U scale (0 for a transition map).
     int seg = 0, c0 = 0, nch = nch_all;
-    bool outputs = true, ident = false;
+    bool ident = false;
     float us = 1.f;
     const float* src = state;
     float* dst = state;
+    float* obuf = nullptr;  // a map's fp32 output rows (from segment 1's first token), or out
     // this head's slots (no slots in the plain job)
     float* segh = job.seg ? job.seg + (size_t)bh * job.nseg * kSegSlots * kSegSlotFloats : nullptr;
     auto slot = [&](int sg, int which) { return segh + ((size_t)sg * kSegSlots + which) * kSegSlotFloats; };
@@ -970,12 +980,8 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
             ident = phi;
             us = phi ? 0.f : 1.f;
             dst = slot(seg, phi ? kSegPhi : kSegZ);
-            outputs = false;
+            obuf = (phi ? job.om : job.oz) + ((size_t)bh * job.Tr + (size_t)(seg - 1) * job.seg_len * kC) * kD;
         }
-    } else if (job.phase == kJobFinish) {
-        seg = unit + 1;
-        src = slot(seg, kSegEntry);
-        dst = seg == job.nseg - 1 ? state : nullptr;
     }
     if (job.phase != kJobPlain) {
         c0 = seg * job.seg_len;
@@ -1024,20 +1030,27 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
         const size_t orow = (size_t)Hv * kD;
         // rows from this workgroup's first chunk on
         half_t* out16 = reinterpret_cast<half_t*>(out) + (size_t)c0 * kC * orow;
-        // fp32 output: row of token t0 + 32 w of chunk ch, column pair * 32
-        float* o32 = reinterpret_cast<float*>(out) + ((size_t)b * T + c0 * kC + 32 * w) * orow + (size_t)h * kD +
-                     pair * 32;
+        // fp32 output (fp32 I/O, or a map's rows in the workspace): row of token t0 + 32 w of
+        // chunk ch, column pair * 32
+        const bool f32out = kF32 || obuf != nullptr;  // uniform
+        const size_t o32_row = obuf ? (size_t)kD : orow;
+        float* o32 = obuf ? obuf + (size_t)(32 * w) * kD + pair * 32
+                          : reinterpret_cast<float*>(out) + ((size_t)b * T + c0 * kC + 32 * w) * orow +
+                                (size_t)h * kD + pair * 32;
         auto step = [&](int slot, int ch) {
-            out_step<TIO>(sm.os[slot], sm.XS[slot], sm.OS[w], w, scale, o32 + (size_t)ch * kC * orow, orow,
-                          Tloc - ch * kC - 32 * w);
+            if (f32out)
+                out_step<float>(sm.os[slot], sm.XS[slot], sm.OS[w], w, scale, o32 + (size_t)ch * kC * o32_row,
+                                o32_row, Tloc - ch * kC - 32 * w);
+            else
+                out_step<TIO>(sm.os[slot], sm.XS[slot], sm.OS[w], w, scale, o32, o32_row, 0);
         };
         for (int it = 0; it <= nch; it += 2) {
-            if (outputs && !kF32 && it >= 2) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 2) * kC, pair, w, Tloc);
-            if (outputs && it >= 1) step(1, it - 1);
+            if (!f32out && it >= 2) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 2) * kC, pair, w, Tloc);
+            if (it >= 1) step(1, it - 1);
             lds_barrier();  // the O stores need not complete before the barrier
             if (it + 1 > nch) break;
-            if (outputs && !kF32 && it >= 1) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 1) * kC, pair, w, Tloc);
-            if (outputs) step(0, it);
+            if (!f32out && it >= 1) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 1) * kC, pair, w, Tloc);
+            step(0, it);
             lds_barrier();
         }
     } else {
@@ -1084,14 +1097,14 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
                 *reinterpret_cast<float4*>(Dg + 16 * m + 4 * g) =
                     lost ? make_float4(nan, nan, nan, nan) : make_float4(S[m][0], S[m][1], S[m][2], S[m][3]);
         }
-    } else if (outw && outputs && !kF32) {
+    } else if (outw && !kF32 && !obuf) {
         out_flush(sm.OS[wave - 2], reinterpret_cast<half_t*>(out) + (size_t)c0 * kC * Hv * kD, b, T, Hv, h,
                   (nch - 1) * kC, pair, wave - 2, Tloc);
     }
 }
 
-// The combine of the sequence split: entry[s + 1] = Phi_s entry[s] + Z_s for s = 1 .. nseg - 2,
-// in fp32.  Slots are stored [column][dk]; row j of the Phi slot is Phi's column j, so with
+// The combine of the sequence split: entry[s + 1] = Phi_s entry[s] + Z_s for s = 1 .. nseg - 1,
+// in fp32; entry[nseg] is the call's final state (state, same layout).  Slots are stored [column][dk]; row j of the Phi slot is Phi's column j, so with
 // E = entry[s] stored the same way, entry[s + 1][c][d] = sum_j E[c][j] Phi[j][d] + Z[c][d].
 // State columns never mix: a workgroup takes R columns of one head through every step and
 // waits for no other workgroup.  Only the E chain is serial: wave w sums over j in
@@ -1101,7 +1114,8 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
 // the host picks the smallest R that keeps about one workgroup per CU.
 constexpr int kCombThreads = 256;
 template <int R>
-__global__ void __launch_bounds__(kCombThreads) gdn_seg_combine(float* __restrict__ seg, int nseg) {
+__global__ void __launch_bounds__(kCombThreads) gdn_seg_combine(float* __restrict__ seg, float* __restrict__ state,
+                                                                int nseg) {
     const int bh = blockIdx.x / (kD / R), c0 = (blockIdx.x % (kD / R)) * R;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     float* segh = seg + (size_t)bh * nseg * kSegSlots * kSegSlotFloats;
@@ -1128,7 +1142,7 @@ __global__ void __launch_bounds__(kCombThreads) gdn_seg_combine(float* __restric
     auto step = [&](int sg, const float2 (&pc)[32], const float (&zc)[kOut], float2 (&pn)[32], float (&zn)[kOut]) {
         // unconditional (the last step reloads its own slot): a branch around the loads would
         // make the compiler wait for them where the paths join
-        const int nx = min(sg + 1, nseg - 2);
+        const int nx = min(sg + 1, nseg - 1);
         quarter(nx, pn);
         zload(nx, zn);
         float2 acc[R] = {};
@@ -1150,7 +1164,7 @@ __global__ void __launch_bounds__(kCombThreads) gdn_seg_combine(float* __restric
 #pragma unroll
         for (int r = 0; r < R; ++r) *reinterpret_cast<float2*>(&part[w][r][2 * lane]) = acc[r];
         __syncthreads();  // partial sums written, E read by every wave
-        float* en = slot(sg + 1, kSegEntry) + (size_t)c0 * kD;
+        float* en = (sg + 1 < nseg ? slot(sg + 1, kSegEntry) : state + (size_t)bh * kSegSlotFloats) + (size_t)c0 * kD;
 #pragma unroll
         for (int i = 0; i < kOut; ++i) {
             const int o = tid + kCombThreads * i, r = o / kD, d = o % kD;
@@ -1167,10 +1181,105 @@ __global__ void __launch_bounds__(kCombThreads) gdn_seg_combine(float* __restric
     quarter(1, pa);
     zload(1, za);
     __syncthreads();
-    for (int sg = 1; sg + 1 < nseg; sg += 2) {
+    for (int sg = 1; sg < nseg; sg += 2) {
         step(sg, pa, za, pb, zb);
-        if (sg + 2 >= nseg) break;
+        if (sg + 1 >= nseg) break;
         step(sg + 1, pb, zb, pa, za);
+    }
+}
+
+// The fixup of the sequence split: O = O_Z + M E^T for the tokens of segments 1 .. nseg-1,
+// every chunk in parallel (a workgroup per (b, h, chunk)).  M [token][dk] and O_Z
+// [token][column] are the map chains' fp32 outputs (scale included), E [column][dk] the
+// entry state of the chunk's segment.  The product runs on fp16 MFMAs with each fp32 operand
+// as an exact hi + lo pair (hi hi + hi lo + lo hi).  E goes to LDS as the B operands' hi and lo
+// halves, rows padded to kFixRow halfs so that the 16 rows one read touches fall in different
+// banks; wave w takes tokens 16 (w % 4) .. + 15 of the chunk and columns 64 (w / 4) .. + 63.
+constexpr int kFixRow = kD + 8;
+constexpr int kFixThreads = 512;
+template <typename TIO>
+__global__ void __launch_bounds__(kFixThreads)
+gdn_seg_fixup(const float* __restrict__ seg, const float* __restrict__ oz, const float* __restrict__ om,
+              TIO* __restrict__ out, int T, int Hv, int nseg, int seg_len, int Tr, int nfix) {
+    const int bh = blockIdx.x / nfix, cl = blockIdx.x % nfix;  // cl: chunk counted from segment 1's start
+    const int b = bh / Hv, h = bh % Hv;
+    const int sg = min(seg_len + cl, nseg * seg_len - 1) / seg_len;  // the chunk's segment (1 .. nseg-1)
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int w = (tid >> 6) & 3, n0 = 4 * (tid >> 8);  // token block; first 16-column tile
+    __shared__ __align__(16) half_t Eh[kD * kFixRow];
+    __shared__ __align__(16) half_t El[kD * kFixRow];
+    // Every global load is issued before any is used (E's 16 float4s per thread, this lane's
+    // M row, its 16 O_Z values), from clamped addresses, and only the stores are guarded: a
+    // load behind a branch, or one per loop trip between LDS stores, waits out its own memory
+    // latency.
+    const float* E = seg + ((size_t)bh * nseg * kSegSlots + (size_t)sg * kSegSlots + kSegEntry) * kSegSlotFloats;
+    constexpr int kEPer = kD * kD / 4 / kFixThreads;  // float4s of E per thread
+    float4 ev[kEPer];
+#pragma unroll
+    for (int i = 0; i < kEPer; ++i) ev[i] = reinterpret_cast<const float4*>(E)[tid + kFixThreads * i];
+    // A operands: this lane's token row of M (rows past T, which the buffers do not hold, read
+    // the last row and are not stored), dk 32 ks + 8 g .. + 7
+    const size_t base = (size_t)bh * Tr;
+    const size_t ra = base + min((size_t)cl * kC + 16 * w + c, (size_t)Tr - 1);
+    float4 mv[4][2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const float4* mp = reinterpret_cast<const float4*>(om + ra * kD + 32 * ks + 8 * g);
+        mv[ks][0] = mp[0];
+        mv[ks][1] = mp[1];
+    }
+    // O_Z of this lane's outputs: tokens 16 w + 4 g + r, columns 16 (n0 + nt) + c
+    float zv[4][4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            zv[nt][r] = oz[(base + min((size_t)cl * kC + 16 * w + 4 * g + r, (size_t)Tr - 1)) * kD + 16 * (n0 + nt) + c];
+#pragma unroll
+    for (int i = 0; i < kEPer; ++i) {
+        const float e4[4] = {ev[i].x, ev[i].y, ev[i].z, ev[i].w};
+        half4_t hv, lv;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            hv[q] = (half_t)e4[q];
+            lv[q] = (half_t)(e4[q] - (float)hv[q]);
+        }
+        const int f = 4 * (tid + kFixThreads * i), row = f / kD, col = f % kD;
+        *reinterpret_cast<half4_t*>(&Eh[row * kFixRow + col]) = hv;
+        *reinterpret_cast<half4_t*>(&El[row * kFixRow + col]) = lv;
+    }
+    half8_t ah[4], al[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const float m8[8] = {mv[ks][0].x, mv[ks][0].y, mv[ks][0].z, mv[ks][0].w,
+                             mv[ks][1].x, mv[ks][1].y, mv[ks][1].z, mv[ks][1].w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            ah[ks][q] = (half_t)m8[q];
+            al[ks][q] = (half_t)(m8[q] - (float)ah[ks][q]);
+        }
+    }
+    __syncthreads();
+    const int t0 = (seg_len + cl) * kC;  // the chunk's first token
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        float4_t acc = {};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int o = (16 * (n0 + nt) + c) * kFixRow + 32 * ks + 8 * g;
+            const half8_t bhv = *reinterpret_cast<const half8_t*>(&Eh[o]);
+            const half8_t blv = *reinterpret_cast<const half8_t*>(&El[o]);
+            acc = mfma16(ah[ks], bhv, acc);
+            acc = mfma16(ah[ks], blv, acc);
+            acc = mfma16(al[ks], bhv, acc);
+        }
+        // acc[r]: token 16 w + 4 g + r, column 16 (n0 + nt) + c
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tl = 16 * w + 4 * g + r;
+            if (t0 + tl < T)
+                out[(((size_t)b * T + t0 + tl) * Hv + h) * kD + 16 * (n0 + nt) + c] = (TIO)(zv[nt][r] + acc[r]);
+        }
     }
 }
 
@@ -1191,30 +1300,30 @@ long env_long(const char* name, long def, long hi) {
 
 // The sequence split of a call: nseg segments of seg_len chunks (nseg == 1: no split).  It pays
 // where the carry's workgroups leave most CUs idle (few heads) and the chunk chain is long.
-// The call's serial time is about 2 (nch / nseg) chunk steps + (nseg - 2) combine steps (a
-// combine step costs about a chunk step), least near nseg = sqrt(2 nch); the plan takes the
-// most segments up to 1.5 sqrt(nch) whose maps launch ((2 nseg - 3) units of 4 workgroups per
-// head) fits in the 256 CUs of the part, each at least kMinSegChunks chunks long.  TSA_GDN_SEGMENTS
-// overrides the choice: 1 never splits, n >= 3 asks for n segments (fewer if the sequence has
+// The call's serial time is about nch / nseg chunk steps (the maps) + nseg - 1 combine steps
+// (each about a chunk step) + the fixup, least near nseg = sqrt(nch); the plan takes the most
+// segments up to sqrt(nch) whose maps launch ((2 nseg - 1) units of 4 workgroups per head)
+// fits in the 256 CUs of the part, each at least kMinSegChunks chunks long.  TSA_GDN_SEGMENTS
+// overrides the choice: 1 never splits, n >= 2 asks for n segments (fewer if the sequence has
 // fewer chunks).  The workspace size follows the plan, so a caller sizes the workspace with
 // the same setting it calls with (the entry points check the size they are given).
 constexpr int kSplitCUs = 256;
-constexpr int kMinSegChunks = 4;
+constexpr int kMinSegChunks = 8;
 struct SegPlan {
     int nseg = 1, seg_len = 0;
 };
 SegPlan seg_plan(int BHv, int nch) {
     const long forced = env_long("TSA_GDN_SEGMENTS", 0, 1 << 20);
     long n = 1;
-    if (forced >= 3)
+    if (forced >= 2)
         n = std::min<long>(forced, nch);
     else if (forced == 0 && BHv > 0)
-        n = std::min<long>(std::min<long>((kSplitCUs / (4 * BHv) + 3) / 2, nch / kMinSegChunks),
-                           (long)(1.5 * std::sqrt((double)nch)));
-    if (n < 3) return {};
+        n = std::min<long>(std::min<long>((kSplitCUs / (4 * BHv) + 1) / 2, nch / kMinSegChunks),
+                           (long)std::sqrt((double)nch));
+    if (n < 2) return {};
     const int seg_len = (int)((nch + n - 1) / n);
     n = (nch + seg_len - 1) / seg_len;  // no empty segment
-    if (n < 3) return {};
+    if (n < 2) return {};
     return {(int)n, seg_len};
 }
 
@@ -1232,11 +1341,14 @@ size_t gdn_chunked_ws_bytes(int B, int T, int Hv, bool f32) {
     const size_t BHv = (size_t)B * Hv;
     // chunk workspaces, then a ready flag per chunk, then an abort word per carry workgroup,
     // then the sequence split's entry / Z / Phi slots when the call splits
+    // (the slots, then the maps' O_Z and M rows of the tokens after segment 0)
     const SegPlan plan = seg_plan((int)BHv, (int)nch);
     if (plan.nseg == 1)
         return BHv * nch * ((f32 ? kWsChunkF32 : kWsChunk) + sizeof(unsigned)) +
                BHv * (kD / (16 * kStrips)) * sizeof(unsigned);
-    return seg_offset(BHv, nch, f32) + BHv * plan.nseg * kSegSlots * kSegSlotFloats * sizeof(float);
+    const size_t Tr = (size_t)T - (size_t)plan.seg_len * kC;
+    return seg_offset(BHv, nch, f32) + BHv * plan.nseg * kSegSlots * kSegSlotFloats * sizeof(float) +
+           2 * BHv * Tr * kD * sizeof(float);
 }
 
 namespace {
@@ -1303,19 +1415,27 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
         job.phase = kJobMaps;
         job.nseg = plan.nseg;
         job.seg_len = plan.seg_len;
+        job.Tr = T - plan.seg_len * kC;
         job.seg = reinterpret_cast<float*>(W + seg_offset(BHv, nch, std::is_same<TIO, float>::value));
+        job.oz = job.seg + (size_t)BHv * plan.nseg * kSegSlots * kSegSlotFloats;
+        job.om = job.oz + (size_t)BHv * job.Tr * kD;
         hipError_t e = prep(stream);
-        if (e == hipSuccess) e = carry(kCarryInOrder, wait_ticks, 2 * plan.nseg - 3, job);
+        if (e == hipSuccess) e = carry(kCarryInOrder, wait_ticks, 2 * plan.nseg - 1, job);
         if (e == hipSuccess) {
             // state columns per combine workgroup: about one workgroup per CU
             const int rows = BHv <= 2 ? 1 : BHv <= 4 ? 2 : BHv <= 8 ? 4 : 8;
             auto combine = rows == 1 ? gdn_seg_combine<1> : rows == 2 ? gdn_seg_combine<2>
                          : rows == 4 ? gdn_seg_combine<4> : gdn_seg_combine<8>;
-            hipLaunchKernelGGL(combine, dim3(BHv * (kD / rows)), dim3(kCombThreads), 0, stream, job.seg, plan.nseg);
+            hipLaunchKernelGGL(combine, dim3(BHv * (kD / rows)), dim3(kCombThreads), 0, stream, job.seg, state,
+                               plan.nseg);
             e = hipGetLastError();
         }
-        job.phase = kJobFinish;
-        if (e == hipSuccess) e = carry(kCarryInOrder, wait_ticks, plan.nseg - 1, job);
+        if (e == hipSuccess) {
+            const int nfix = nch - plan.seg_len;
+            hipLaunchKernelGGL(gdn_seg_fixup<TIO>, dim3(BHv * nfix), dim3(kFixThreads), 0, stream, job.seg, job.oz,
+                               job.om, static_cast<TIO*>(out), T, Hv, plan.nseg, plan.seg_len, job.Tr, nfix);
+            e = hipGetLastError();
+        }
         return e;
     }
 

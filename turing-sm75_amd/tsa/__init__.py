@@ -260,7 +260,7 @@ def gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk=128, dv=128, chunk=64, f32=Fals
 def gdn_chunked_fwd(q, k, v, g_log, beta, state, out=None, scale=None, chunk=64, ws=None,
                     stream=None):
     """Chunked prefill; state [B, Hv, dv, dk] is updated in place; returns out.  fp32 q/k/v
-    select tsa_gdn_chunked_fwd_f32 (fp32 out).  With few heads (B*Hv <= 21) and at least 12
+    select tsa_gdn_chunked_fwd_f32 (fp32 out).  With few heads (B*Hv <= 21) and at least 16
     chunks the library splits the sequence into segments run side by side (same results to
     fp32 rounding)."""
     import torch
