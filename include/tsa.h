@@ -125,10 +125,12 @@ int tsa_gdn_chunked_fwd_f32(const float* q, const float* k, const float* v, cons
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference, whose driver allocates the two-pass scratch
  * itself (src/gdn_sm75.cu:1341-1346).  The workspace is a fixed 64 MiB device array inside
- * the library, one per GPU, held until the process ends; shapes whose
- * tsa_gdn_chunked_workspace_bytes(...) exceed 64 MiB return TSA_ERR_SCRATCH (e.g. 32 V-heads
- * up to T = 2240).  Nothing is allocated, no stream or event is created (the kernels run
- * in order on `stream`), and the results equal tsa_gdn_chunked_fwd's.  Every call on a GPU
+ * the library, one per GPU, held until the process ends.  The call splits the sequence (as
+ * tsa_gdn_chunked_fwd does with few heads) only where the split's larger workspace fits there,
+ * and otherwise runs the chunk carry whole; shapes whose workspace exceeds 64 MiB even so
+ * return TSA_ERR_SCRATCH (e.g. 32 V-heads up to T = 2240).  Nothing is allocated, no stream
+ * or event is created (the kernels run in order on `stream`), and the results equal
+ * tsa_gdn_chunked_fwd's bit for bit whenever both take the same plan.  Every call on a GPU
  * uses that GPU's one array: calls that overlap on one GPU (other streams, other host
  * threads) race and must be ordered by the caller. */
 int tsa_gdn_chunked_fwd_noalloc(const void* q, const void* k, const void* v, const float* g_log,

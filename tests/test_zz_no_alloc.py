@@ -68,3 +68,31 @@ def test_noalloc_sequence_split(dev, monkeypatch):
         monkeypatch.delenv("TSA_GDN_SEGMENTS")
     _case(dev, 15, 1, 2048, 2, 4)
     _case(dev, 16, 1, 1000, 1, 2)
+
+
+def test_noalloc_runs_whole_where_the_split_does_not_fit(dev, monkeypatch):
+    """4 V-heads, T = 9000: the split's workspace (71 MB) exceeds the 64 MiB scratch, so the
+    no-allocation call runs the chunk carry whole (33 MB) instead of failing; it equals the
+    workspace entry point with the split turned off, bit for bit."""
+    import torch
+    monkeypatch.delenv("TSA_GDN_SEGMENTS", raising=False)
+    B, T, Hq, Hv = 1, 9000, 2, 4
+    assert tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv) > 64 << 20
+    monkeypatch.setenv("TSA_GDN_SEGMENTS", "1")
+    assert tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv) <= 64 << 20
+    print(f"no-alloc case B={B} T={T} Hq={Hq} Hv={Hv}, whole carry", flush=True)
+    rng = np.random.default_rng(17)
+    q, k, v, g, beta, st = (torch.from_numpy(a).to(dev) for a in _inputs(rng, B, T, Hq, Hv))
+    s_ref = st.clone()
+    o_ref = tsa.gdn_chunked_fwd(q, k, v, g, beta, s_ref)  # split off
+    torch.cuda.synchronize()
+    monkeypatch.delenv("TSA_GDN_SEGMENTS")
+    s_new, o_new = st.clone(), torch.empty_like(v)
+    stream = torch.cuda.current_stream()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = tsa.load().tsa_gdn_chunked_fwd_noalloc(
+        p(q), p(k), p(v), p(g), p(beta), p(s_new), p(o_new), B, T, Hq, Hv, D, D, 64,
+        1.0 / math.sqrt(D), ctypes.c_void_p(stream.cuda_stream))
+    assert rc == tsa.TSA_OK, tsa.strerror(rc)
+    torch.cuda.synchronize()
+    assert torch.equal(o_new, o_ref) and torch.equal(s_new, s_ref)

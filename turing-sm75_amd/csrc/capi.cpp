@@ -168,7 +168,7 @@ extern "C" int tsa_gdn_chunked_fwd_noalloc(const void* q, const void* k, const v
     if (dk != 128 || dv != 128 || chunk != 64) return TSA_ERR_UNSUPPORTED;
     const long long nch = (T + 63LL) / 64;
     if (!fits_int(B, Hv, nch) || !fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
-    if (tsa::gdn_chunked_ws_bytes(B, T, Hv, false) > tsa::gdn_chunked_noalloc_max_bytes()) return TSA_ERR_SCRATCH;
+    if (tsa::gdn_chunked_noalloc_ws_bytes(B, T, Hv) > tsa::gdn_chunked_noalloc_max_bytes()) return TSA_ERR_SCRATCH;
     return from_hip(tsa::gdn_chunked_noalloc(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale,
                                              as_stream(stream)));
 }

@@ -29,6 +29,7 @@
 //   batches ahead of the MFMAs.
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -1336,19 +1337,31 @@ size_t seg_offset(size_t BHv, size_t nch, bool f32) {
 }
 }  // namespace
 
-size_t gdn_chunked_ws_bytes(int B, int T, int Hv, bool f32) {
-    const size_t nch = (size_t)(T + kC - 1) / kC;
-    const size_t BHv = (size_t)B * Hv;
-    // chunk workspaces, then a ready flag per chunk, then an abort word per carry workgroup,
-    // then the sequence split's entry / Z / Phi slots when the call splits
-    // (the slots, then the maps' O_Z and M rows of the tokens after segment 0)
-    const SegPlan plan = seg_plan((int)BHv, (int)nch);
+namespace {
+// Workspace bytes of a call under a plan: chunk workspaces, then a ready flag per chunk, then
+// an abort word per carry workgroup, then, when the call splits, the slots and the maps' O_Z
+// and M rows of the tokens after segment 0
+size_t ws_bytes_for(size_t BHv, size_t nch, int T, bool f32, const SegPlan& plan) {
     if (plan.nseg == 1)
         return BHv * nch * ((f32 ? kWsChunkF32 : kWsChunk) + sizeof(unsigned)) +
                BHv * (kD / (16 * kStrips)) * sizeof(unsigned);
     const size_t Tr = (size_t)T - (size_t)plan.seg_len * kC;
     return seg_offset(BHv, nch, f32) + BHv * plan.nseg * kSegSlots * kSegSlotFloats * sizeof(float) +
            2 * BHv * Tr * kD * sizeof(float);
+}
+
+// The plan of a call whose workspace holds at most `budget` bytes: the split where it fits,
+// else none (the no-allocation entry's fixed scratch).
+SegPlan call_plan(int BHv, int nch, int T, bool f32, size_t budget) {
+    SegPlan plan = seg_plan(BHv, nch);
+    if (plan.nseg > 1 && ws_bytes_for((size_t)BHv, (size_t)nch, T, f32, plan) > budget) plan = SegPlan{};
+    return plan;
+}
+}  // namespace
+
+size_t gdn_chunked_ws_bytes(int B, int T, int Hv, bool f32) {
+    const int nch = (T + kC - 1) / kC, BHv = B * Hv;
+    return ws_bytes_for((size_t)BHv, (size_t)nch, T, f32, call_plan(BHv, nch, T, f32, SIZE_MAX));
 }
 
 namespace {
@@ -1380,7 +1393,7 @@ template <bool kFused, typename TIO>
 hipError_t launch_chunked(const void* q, const void* k, const void* v, const float* g_log,
                           const float* beta, const GdnRawGates& gates, float* state, void* out,
                           int B, int T, int Hq, int Hv, float scale, void* ws, bool may_overlap,
-                          hipStream_t stream) {
+                          hipStream_t stream, size_t ws_budget = SIZE_MAX) {
     const int nch = (T + kC - 1) / kC;
     const int BHv = B * Hv;
     const int carry_wgs = BHv * (kD / (16 * kStrips));
@@ -1409,7 +1422,7 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
     };
 
     // Sequence split: in order on the caller's stream (the maps need every chunk's operands)
-    const SegPlan plan = seg_plan(BHv, nch);
+    const SegPlan plan = call_plan(BHv, nch, T, std::is_same<TIO, float>::value, ws_budget);
     if (plan.nseg > 1) {
         CarryJob job;
         job.phase = kJobMaps;
@@ -1531,6 +1544,12 @@ hipError_t scratch_address(hipStream_t stream, void** out) {
 
 size_t gdn_chunked_noalloc_max_bytes() { return kScratchBytes; }
 
+// The no-allocation entry splits the sequence only where the split's workspace fits the scratch.
+size_t gdn_chunked_noalloc_ws_bytes(int B, int T, int Hv) {
+    const int nch = (T + kC - 1) / kC, BHv = B * Hv;
+    return ws_bytes_for((size_t)BHv, (size_t)nch, T, false, call_plan(BHv, nch, T, false, kScratchBytes));
+}
+
 hipError_t gdn_chunked_noalloc(const void* q, const void* k, const void* v, const float* g_log,
                                const float* beta, float* state, void* out, int B, int T, int Hq,
                                int Hv, float scale, hipStream_t stream) {
@@ -1539,7 +1558,7 @@ hipError_t gdn_chunked_noalloc(const void* q, const void* k, const void* v, cons
     if (e != hipSuccess) return e;
     // in order on the caller's stream: no side stream or event is ever created here
     return launch_chunked<false, half_t>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq, Hv,
-                                         scale, ws, false, stream);
+                                         scale, ws, false, stream, kScratchBytes);
 }
 
 hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, bool f32, int* count,

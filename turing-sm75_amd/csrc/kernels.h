@@ -36,6 +36,8 @@ hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float*
 // (gdn_chunked_noalloc_max_bytes() bytes per GPU) stands in for it; no allocation, no side
 // stream.  The caller checks gdn_chunked_ws_bytes(...) against the maximum.
 size_t gdn_chunked_noalloc_max_bytes();
+// Workspace bytes of a no-allocation call: it splits the sequence only where that fits.
+size_t gdn_chunked_noalloc_ws_bytes(int B, int T, int Hv);
 hipError_t gdn_chunked_noalloc(const void* q, const void* k, const void* v, const float* g_log,
                                const float* beta, float* state, void* out, int B, int T, int Hq,
                                int Hv, float scale, hipStream_t stream);
