@@ -1,0 +1,79 @@
+"""GPU parity over a seeded sweep of shapes: the chunked prefill (fp16 and fp32 I/O, with and
+without the sequence split, the split's segment count forced or left to the library) and the
+token-serial kernel against the oracle's serial recurrence (gdn_cpu, src/gdn_sm75.cu:1078-1106)
+on the same inputs.  Shapes mix batches, ragged T (from one token to past 14 chunks), QK and V
+head counts in any relation (Hv < Hq, Hv % Hq != 0), fast and slow gates and a nonzero
+entering state, so that index arithmetic of every launch (prep, carry, maps, combine, fixup)
+meets shapes the hand-picked cases do not.
+
+Gates: outputs max-abs < 0.02 (src/gdn_sm75.cu:1313), state within 1e-3 relative; tighter
+per-kernel bounds as in test_gpu_gdn.py (the slow gate, whose entering state still weighs at
+the end of the sequence, at 8e-4 for the chunked state).
+"""
+import numpy as np
+import pytest
+
+import tsa
+
+pytestmark = pytest.mark.gpu
+D = 128
+OUT_GATE, STATE_GATE = 2e-2, 1e-3
+
+
+def _cases(n=24, seed=2026):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        B = int(rng.integers(1, 4))
+        T = int(rng.choice([1, 2, 31, 64, 65]) if i % 4 == 0 else rng.integers(66, 920))
+        Hq = int(rng.integers(1, 5))
+        Hv = int(rng.integers(1, 9))
+        f32 = bool(i % 3 == 1)
+        slow = bool(i % 2 == 1)
+        segs = [None, "1", "2", "3", "5"][i % 5]
+        cases.append((i, B, T, Hq, Hv, f32, slow, segs))
+    return cases
+
+
+def _inputs(rng, B, T, Hq, Hv, slow):
+    l2n = lambda x: x / np.linalg.norm(x, axis=-1, keepdims=True)
+    q = l2n(rng.standard_normal((B, T, Hq, D))).astype(np.float16)
+    k = l2n(rng.standard_normal((B, T, Hq, D))).astype(np.float16)
+    v = rng.standard_normal((B, T, Hv, D)).astype(np.float16)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((B, T, Hv))))).astype(np.float32)
+    if slow:
+        g = (-0.002 * (1 + 0.5 * rng.standard_normal((B, T, Hv)))).astype(np.float32)
+    else:
+        g = (-np.logaddexp(0.0, rng.standard_normal((B, T, Hv)))).astype(np.float32)
+    st = (0.02 * rng.standard_normal((B, Hv, D, D))).astype(np.float32)
+    return q, k, v, g, beta, st
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: "c{}_B{}T{}Hq{}Hv{}{}{}s{}".format(
+    c[0], c[1], c[2], c[3], c[4], "_f32" if c[5] else "", "_slow" if c[6] else "", c[7]))
+def test_shape_sweep(dev, orc, monkeypatch, case):
+    import torch
+    i, B, T, Hq, Hv, f32, slow, segs = case
+    if segs is None:
+        monkeypatch.delenv("TSA_GDN_SEGMENTS", raising=False)
+    else:
+        monkeypatch.setenv("TSA_GDN_SEGMENTS", segs)
+    print(f"sweep case {i}: B={B} T={T} Hq={Hq} Hv={Hv} f32={f32} slow={slow} segments={segs}", flush=True)
+    rng = np.random.default_rng(1000 + i)
+    arrays = _inputs(rng, B, T, Hq, Hv, slow)
+    if f32:
+        arrays = tuple(a.astype(np.float32) for a in arrays)
+    o_ref, s_ref = orc.gdn_serial(*arrays)
+    scale = float(np.abs(s_ref).max())
+    for kind in ("chunked", "recurrent"):
+        tq, tk, tv, tg, tb, ts = (torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in arrays)
+        fn = tsa.gdn_chunked_fwd if kind == "chunked" else tsa.gdn_recurrent_fwd
+        o = fn(tq, tk, tv, tg, tb, ts)
+        torch.cuda.synchronize()
+        assert o.dtype == (torch.float32 if f32 else torch.float16)
+        eo = float(np.abs(o.float().cpu().numpy() - o_ref).max())
+        es = float(np.abs(ts.cpu().numpy() - s_ref).max() / max(scale, 1e-30))
+        print(f"  {kind}: out max-abs {eo:.2e}  state rel {es:.2e}", flush=True)
+        out_tol = 2e-3
+        state_tol = (8e-4 if slow else 3e-4) if kind == "chunked" else 1e-5
+        assert eo < min(out_tol, OUT_GATE) and es < min(state_tol, STATE_GATE)
