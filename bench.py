@@ -358,6 +358,41 @@ def cpu_baselines(torch, a, pre, dec, threads, lay=None):
     return res
 
 
+def dispatch_sweep(torch, tsa, dev, stream, Hq=16, Hv=48, d=128, reps=20):
+    """Token-serial (tsa_gdn_recurrent_fwd) vs chunked (tsa_gdn_chunked_fwd) time per call at
+    the reference's head counts, for the short sequences where the ggml adapter switches from
+    one to the other (T < 32 token-serial, else chunked).  HIP events around `reps` calls of
+    each kernel, in order B, T, kernel; fp16 q/k/v, gates as the prefill's."""
+    rows = []
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    for B in (1, 4):
+        for T in (8, 16, 24, 32, 40, 48, 64, 96):
+            l2n = lambda x: x / x.norm(dim=-1, keepdim=True)
+            q = l2n(torch.randn(B, T, Hq, d, device=dev, generator=g)).half()
+            k = l2n(torch.randn(B, T, Hq, d, device=dev, generator=g)).half()
+            v = torch.randn(B, T, Hv, d, device=dev, generator=g).half()
+            gl = -torch.nn.functional.softplus(torch.randn(B, T, Hv, device=dev, generator=g))
+            beta = torch.sigmoid(torch.randn(B, T, Hv, device=dev, generator=g))
+            st = torch.zeros(B, Hv, d, d, device=dev)
+            out = torch.empty_like(v)
+            ws = torch.empty(tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv), dtype=torch.uint8, device=dev)
+            row = {"B": B, "T": T}
+            for name, fn in (("token_serial", lambda: tsa.gdn_recurrent_fwd(q, k, v, gl, beta, st, out, stream=stream)),
+                             ("chunked", lambda: tsa.gdn_chunked_fwd(q, k, v, gl, beta, st, out, ws=ws, stream=stream))):
+                fn()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(reps):
+                    fn()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                row["us_" + name] = round(e0.elapsed_time(e1) / reps * 1e3, 2)
+            rows.append(row)
+    return {"dispatch_sweep": rows, "heads": {"Hq": Hq, "Hv": Hv}, "reps": reps,
+            "adapter_rule": "T = 1 decode step, T < 32 token-serial, else chunked"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -369,6 +404,10 @@ def main():
     ap.add_argument("--no-sustained", action="store_true",
                     help="skip the sustained attention run and the GEMM reference (~5 s; under a "
                          "profiler their launches would outnumber the step's)")
+    ap.add_argument("--dispatch-sweep", action="store_true",
+                    help="only time the token-serial and the chunked GDN kernels at 16 QK / 48 V "
+                         "heads for B = 1, 4 and T = 8 .. 96 (the ggml adapter's dispatch "
+                         "threshold) and print that table as one JSON line")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the measurements, run one plain copy kernel over this many MiB "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -387,6 +426,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
+    if args.dispatch_sweep:
+        print(json.dumps(dispatch_sweep(torch, tsa, dev, stream)))
+        return 0
     a, pre, dec = make_inputs(torch, dev)
     ws = torch.empty(tsa.gdn_chunked_workspace_bytes(PREFILL["B"], PREFILL["T"], PREFILL["Hq"],
                                                      PREFILL["Hv"]), dtype=torch.uint8, device=dev)
