@@ -16,8 +16,11 @@ The decode part's figure is the decode workload itself, timed after the step: 51
 steps back to back, each with its own pre-generated token (fresh q, k, v, g, beta per step),
 cycling the 16 replicas, between one pair of events (a serving loop's step time, not one
 launch's latency); the 16 in-step launches are reported beside it.
-W untimed warmup steps (default 50, grouped by part with attention last: the board's power
-management needs ~12 ms of continuous attention to settle), then exactly K timed steps
+W untimed warmup steps (default 50, grouped by part with attention last; attention itself
+always gets at least ATTN_MIN_WARMUP launches back to back, ~45 ms, whatever W is: after an
+idle gap the board's power management needs ~12 ms of continuous attention to settle, and a
+timed loop inside that transient measures the power controller, not the kernel), then
+exactly K timed steps
 between two synchronisations, their work grouped by part (K attention launches back to
 back, then K prefills, then the K x 16 decode launches), so each kernel is timed in its own
 loop as the reference's lab drivers time theirs: a part's average launch duration is one
@@ -61,6 +64,9 @@ sys.path.insert(0, os.path.join(ROOT, "turing-sm75_amd"))
 
 PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA (no sparsity)
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+# continuous attention launches right before the timed region, whatever --warmup is (~45 ms
+# at config 3; the power controller's start-up transient lasts ~12 ms)
+ATTN_MIN_WARMUP = 80
 
 # configuration of each part
 ATTN = dict(B=1, H=32, S=8192, D=128, causal=True)
@@ -471,9 +477,11 @@ def main():
     # starts under the load it measures: after an idle gap or a lighter kernel the board's
     # power management overshoots on the first ~12 ms of attention (launches 4-20 measured at
     # 630-700 us against a steady ~555 us), a transient of the power controller, not of the
-    # kernel.  The default 50 warm-up steps give attention ~28 ms of continuous load.
-    for _, fn in parts[1:] + parts[:1]:
-        for _ in range(args.warmup):
+    # kernel.  Attention gets at least ATTN_MIN_WARMUP launches (~45 ms of continuous load)
+    # whatever --warmup asks for; the other parts get --warmup steps each.
+    attn_warm = max(args.warmup, ATTN_MIN_WARMUP)
+    for name, fn in parts[1:] + parts[:1]:
+        for _ in range(attn_warm if name == "attn_fwd" else args.warmup):
             fn()
     torch.cuda.synchronize()
 
@@ -684,7 +692,7 @@ def main():
         "attn_fwd": {
             "workload": "attention fwd B=1 H=32 S=8192 D=128 causal fp16, N(0,0.5) + 1% x8 outliers",
             "value": round(attn_tflops, 2), "unit": "TFLOP/s", "ms": round(ms["attn_fwd"], 5),
-            "flop_per_launch": fa,
+            "flop_per_launch": fa, "warmup_launches": attn_warm,
             "roofline": roof("mfma", attn_tflops, PEAK_MFMA_F16_TFLOPS, "TFLOP/s", "attn_fwd"),
         },
         "gdn_prefill": {
