@@ -588,7 +588,7 @@ def main():
     # context: one GPU's share of the prefill under 8-way head sharding (Hq=2, Hv=4 of the
     # 16 / 32 heads).  With so few heads the chunk carry alone would leave most CUs idle, so
     # the call splits the sequence (segment state maps side by side, a combine, a fix-up);
-    # the same call with the split turned off (TSA_GDN_SEGMENTS=1) is timed beside it.
+    # the same call with the split turned off (an explicit plan of one segment) is timed beside it.
     shq, shv = PREFILL["Hq"] // 8, PREFILL["Hv"] // 8
     sq, sk = (x[:, :, :shq].contiguous() for x in (pre["q"], pre["k"]))
     sv = pre["v"][:, :, :shv].contiguous()
@@ -596,29 +596,21 @@ def main():
     sst = torch.zeros(PREFILL["B"], shv, PREFILL["d"], PREFILL["d"], device=dev)
     so = torch.empty_like(sv)
 
-    def shard_ms(segments):
-        old = os.environ.pop("TSA_GDN_SEGMENTS", None)
-        if segments is not None:
-            os.environ["TSA_GDN_SEGMENTS"] = segments
-        try:
-            nbytes = tsa.gdn_chunked_workspace_bytes(PREFILL["B"], PREFILL["T"], shq, shv)
-            sws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    def shard_ms(nseg):
+        nbytes = tsa.gdn_chunked_workspace_bytes(PREFILL["B"], PREFILL["T"], shq, shv, nseg=nseg)
+        sws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
 
-            def f():
-                sst.zero_()
-                tsa.gdn_chunked_fwd(sq, sk, sv, sg, sb, sst, so, ws=sws, stream=stream)
-            return time_fn(f, n_lay), nbytes
-        finally:
-            os.environ.pop("TSA_GDN_SEGMENTS", None)
-            if old is not None:
-                os.environ["TSA_GDN_SEGMENTS"] = old
+        def f():
+            sst.zero_()
+            tsa.gdn_chunked_fwd(sq, sk, sv, sg, sb, sst, so, ws=sws, stream=stream, nseg=nseg)
+        return time_fn(f, n_lay), nbytes
 
     def shard_zero():
         sst.zero_()
 
     shard_zero_ms = time_fn(shard_zero, n_lay)
-    shard_split_ms, shard_ws = shard_ms(None)
-    shard_plain_ms, shard_ws_plain = shard_ms("1")
+    shard_split_ms, shard_ws = shard_ms(0)
+    shard_plain_ms, shard_ws_plain = shard_ms(1)
     shard_split_ms -= shard_zero_ms
     shard_plain_ms -= shard_zero_ms
 

@@ -5,13 +5,13 @@
  * takes device pointers to contiguous buffers the caller owns, enqueues work on the
  * given HIP stream (NULL = the default stream) and returns at once: no device memory is
  * allocated and nothing is synchronised (tsa_gdn_chunked_redo_count, a diagnostic, is the
- * one synchronous call).  The one piece of process-wide state: the chunked prefill
- * (tsa_gdn_chunked_fwd and its fused form) runs its two kernels side by side on the
- * caller's stream and on a second stream of the same device, which it creates with two
- * events on the first such call on that device (under a mutex) and keeps until the process
- * ends; the environment variable TSA_GDN_OVERLAP=0 keeps both kernels on the caller's stream
- * and creates nothing.  Errors come back as TSA_* codes, never as exit() or exceptions (the
- * reference's CUDA_CHECK exits, src/attn_sm75.cu:40-48).
+ * one synchronous call).  Every kernel runs on the caller's stream, in order, as the
+ * reference's launches run on one stream with caller-owned scratch (src/gdn_sm75.cu:1341-1346).
+ * Opt-in only: with the environment variable TSA_GDN_OVERLAP=1 the chunked prefill (not under
+ * graph capture) runs its two kernels side by side on the caller's stream and on a second
+ * stream of the same device, which it creates with two events on the first such call on that
+ * device (under a mutex) and keeps until the process ends.  Errors come back as TSA_* codes,
+ * never as exit() or exceptions (the reference's CUDA_CHECK exits, src/attn_sm75.cu:40-48).
  *
  * dtypes: q/k/v/o/out are IEEE fp16 (passed as void*), g_log, beta and the GDN state are
  * fp32; the *_f32 GDN entry points take q/k/v/out in fp32 as well, the reference's own GDN
@@ -94,14 +94,14 @@ int tsa_attn_gqa_naive(const void* q, const void* k, const void* v, const void* 
  * :271-292, is only first-order accurate).  dk = dv = 128, chunk = 64.  ws must hold
  * tsa_gdn_chunked_workspace_bytes(...) bytes of device memory, the caller's as the
  * reference driver owns the two-pass scratch (src/gdn_sm75.cu:1341-1346); its contents on
- * entry do not matter (a call whose two kernels run side by side clears its ready flags
- * first; one that runs them in order needs no clear), and calls that share one ws must be
- * ordered on one stream.  With few heads and many chunks (B*Hv <= 21, at least 16 chunks)
- * the call splits the sequence into segments (segment state maps with their outputs side by
- * side, a combine, a parallel output fix-up) and the workspace grows by 192 KiB per head and
- * segment and 1 KiB per head and token after the first segment; the environment variable
- * TSA_GDN_SEGMENTS, read by both functions, overrides that plan (1: never split, n >= 2:
- * n segments), so a caller sizes ws under the setting it calls with. */
+ * entry do not matter (the prep writes every ready flag the carry reads; a call whose two
+ * kernels run side by side, TSA_GDN_OVERLAP=1, clears them first), and calls that share one
+ * ws must be ordered on one stream.  With few heads and many chunks (B*Hv <= 21, at least 16
+ * chunks) the call splits the sequence into segments (segment state maps with their outputs
+ * side by side, a combine, a parallel output fix-up) and the workspace grows by 192 KiB per
+ * head and segment and 1 KiB per head and token after the first segment.  The plan, and so
+ * the workspace size, is a function of the shapes only; tsa_gdn_chunked_plan_fwd takes an
+ * explicit one. */
 size_t tsa_gdn_chunked_workspace_bytes(int B, int T, int Hq, int Hv, int dk, int dv,
                                        int chunk);
 int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v, const float* g_log,
@@ -121,10 +121,24 @@ int tsa_gdn_chunked_fwd_f32(const float* q, const float* k, const float* v, cons
                             int Hv, int dk, int dv, int chunk, float scale, void* ws,
                             size_t ws_bytes, void* stream);
 
+/* The chunked prefill with an explicit sequence-split plan (no counterpart in the reference,
+ * which carries the state through every chunk in order): nseg = 0 takes the library's plan,
+ * the one tsa_gdn_chunked_fwd uses; nseg = 1 never splits; nseg >= 2 asks for nseg segments
+ * (fewer when the sequence has fewer chunks, so that no segment is empty).  io_f32 = 1: q, k,
+ * v, out are fp32 as in tsa_gdn_chunked_fwd_f32, else fp16.  ws must hold
+ * tsa_gdn_chunked_plan_workspace_bytes(..., io_f32, nseg) bytes (0 for invalid arguments).
+ * Results equal tsa_gdn_chunked_fwd's whenever the plans agree; otherwise they agree to fp32
+ * rounding. */
+size_t tsa_gdn_chunked_plan_workspace_bytes(int B, int T, int Hq, int Hv, int dk, int dv,
+                                            int chunk, int io_f32, int nseg);
+int tsa_gdn_chunked_plan_fwd(const void* q, const void* k, const void* v, const float* g_log,
+                             const float* beta, float* state, void* out, int B, int T, int Hq,
+                             int Hv, int dk, int dv, int chunk, float scale, int io_f32, int nseg,
+                             void* ws, size_t ws_bytes, void* stream);
+
 /* tsa_gdn_chunked_fwd without a workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  No counterpart in the reference, whose driver allocates the two-pass scratch
- * itself (src/gdn_sm75.cu:1341-1346).  The workspace is a fixed 64 MiB device array inside
+ * hipMalloc).  No counterpart in the reference.  The workspace is a fixed 64 MiB device array inside
  * the library, one per GPU, held until the process ends.  The call splits the sequence (as
  * tsa_gdn_chunked_fwd does with few heads) only where the split's larger workspace fits there,
  * and otherwise runs the chunk carry whole; shapes whose workspace exceeds 64 MiB even so
@@ -138,11 +152,12 @@ int tsa_gdn_chunked_fwd_noalloc(const void* q, const void* k, const void* v, con
                                 int Hv, int dk, int dv, int chunk, float scale, void* stream);
 
 /* Diagnostic, no reference counterpart: after a tsa_gdn_chunked_fwd (fused, or with io_f32 = 1
- * tsa_gdn_chunked_fwd_f32) call on ws with these shapes, *count = the number of its
- * state-carrying workgroups that waited longer than the limit for the side-by-side kernel (a
- * scheduler that did not run the two kernels together) and were redone by the call's second
- * launch; 0 when the overlap worked.  Synchronises `stream` (a device-to-host copy of the
- * call's abort words). */
+ * tsa_gdn_chunked_fwd_f32) call on ws with these shapes that ran side by side
+ * (TSA_GDN_OVERLAP=1), *count = the number of its state-carrying workgroups that waited longer
+ * than the limit for the side-by-side kernel (a scheduler that did not run the two kernels
+ * together) and were redone by the call's second launch; 0 when the overlap worked, and after
+ * a call in order (the default).  Synchronises `stream` (a device-to-host copy of the call's
+ * abort words). */
 int tsa_gdn_chunked_redo_count(const void* ws, size_t ws_bytes, int B, int T, int Hq, int Hv,
                                int dk, int dv, int chunk, int io_f32, int* count, void* stream);
 

@@ -129,42 +129,60 @@ def test_gdn_workspace_bytes_scales_with_chunks():
     assert tsa.gdn_chunked_workspace_bytes(1, 64, 16, 32, chunk=32) == 0
 
 
-def test_gdn_workspace_bytes_with_sequence_split(monkeypatch):
+def test_gdn_workspace_bytes_with_sequence_split():
     # few heads and many chunks split the sequence: after the flags and abort words, at a
     # 256-byte boundary, three 64 KiB fp32 slots (entry state, Z, Phi) per head and segment,
     # then per head two fp32 rows of 128 (the maps' O_Z and M) per token after segment 0
-    monkeypatch.delenv("TSA_GDN_SEGMENTS", raising=False)
     base = lambda BHv, nch: BHv * (nch * (58368 + 4) + 4 * 4)
     rows = lambda BHv, T, L: 2 * BHv * (T - 64 * L) * 512
     split = lambda BHv, nch, nseg, T, L: ((base(BHv, nch) + 255) // 256 * 256 + BHv * nseg * 3 * 65536 +
                                            rows(BHv, T, L))
+    ws = tsa.gdn_chunked_workspace_bytes
     # 4 heads, 64 chunks: 8 segments of 8 chunks (the maps launch, 15 units x 4 workgroups x
     # 4 heads, fits 256 CUs; sqrt(64) = 8)
-    assert tsa.gdn_chunked_workspace_bytes(1, 4096, 2, 4) == split(4, 64, 8, 4096, 8)
+    assert ws(1, 4096, 2, 4) == split(4, 64, 8, 4096, 8)
     # 1 head: 8 segments at 64 chunks, 16 of 16 chunks at 256, 2 of 8 at 16 (8 chunks at least)
-    assert tsa.gdn_chunked_workspace_bytes(1, 4096, 1, 1) == split(1, 64, 8, 4096, 8)
-    assert tsa.gdn_chunked_workspace_bytes(1, 16384, 1, 1) == split(1, 256, 16, 16384, 16)
-    assert tsa.gdn_chunked_workspace_bytes(1, 1024, 1, 1) == split(1, 16, 2, 1024, 8)
+    assert ws(1, 4096, 1, 1) == split(1, 64, 8, 4096, 8)
+    assert ws(1, 16384, 1, 1) == split(1, 256, 16, 16384, 16)
+    assert ws(1, 1024, 1, 1) == split(1, 16, 2, 1024, 8)
     # 16 heads: 2 segments (3 units x 64 workgroups); 32 heads: the carry already takes half
     # the CUs, no split; 11 chunks: too short to split
-    assert tsa.gdn_chunked_workspace_bytes(1, 4096, 8, 16) == split(16, 64, 2, 4096, 32)
-    assert tsa.gdn_chunked_workspace_bytes(1, 4096, 16, 32) == base(32, 64)
-    assert tsa.gdn_chunked_workspace_bytes(1, 704, 2, 4) == base(4, 11)
-    monkeypatch.setenv("TSA_GDN_SEGMENTS", "1")
-    assert tsa.gdn_chunked_workspace_bytes(1, 4096, 2, 4) == base(4, 64)
-    monkeypatch.setenv("TSA_GDN_SEGMENTS", "3")
-    assert tsa.gdn_chunked_workspace_bytes(1, 1000, 1, 2) == split(2, 16, 3, 1000, 6)  # 6 + 6 + 4
-    assert tsa.gdn_chunked_workspace_bytes(1, 128, 1, 2) == split(2, 2, 2, 128, 1)  # 2 chunks: 2 of 1
-    assert tsa.gdn_chunked_workspace_bytes(1, 64, 1, 2) == base(2, 1)  # 1 chunk: no split
-    monkeypatch.setenv("TSA_GDN_SEGMENTS", "5")
-    assert tsa.gdn_chunked_workspace_bytes(2, 777, 3, 4) == split(8, 13, 5, 777, 3)  # 3 x 4 + 1
-    monkeypatch.setenv("TSA_GDN_SEGMENTS", "1000")
-    assert tsa.gdn_chunked_workspace_bytes(2, 777, 3, 4) == split(8, 13, 13, 777, 1)  # one chunk each
-    monkeypatch.setenv("TSA_GDN_SEGMENTS", "4")
+    assert ws(1, 4096, 8, 16) == split(16, 64, 2, 4096, 32)
+    assert ws(1, 4096, 16, 32) == base(32, 64)
+    assert ws(1, 704, 2, 4) == base(4, 11)
+    # the library's plan is a function of the shapes: nseg = 0 is the same query
+    for shape in ((1, 4096, 2, 4), (1, 4096, 16, 32), (1, 1024, 1, 1)):
+        assert ws(*shape, nseg=0) == ws(*shape)
+        assert ws(*shape, f32=True, nseg=0) == ws(*shape, f32=True)
+    # explicit plans
+    assert ws(1, 4096, 2, 4, nseg=1) == base(4, 64)
+    assert ws(1, 1000, 1, 2, nseg=3) == split(2, 16, 3, 1000, 6)  # 6 + 6 + 4
+    assert ws(1, 128, 1, 2, nseg=3) == split(2, 2, 2, 128, 1)  # 2 chunks: 2 of 1
+    assert ws(1, 64, 1, 2, nseg=3) == base(2, 1)  # 1 chunk: no split
+    assert ws(2, 777, 3, 4, nseg=5) == split(8, 13, 5, 777, 3)  # 3 x 4 + 1
+    assert ws(2, 777, 3, 4, nseg=1000) == split(8, 13, 13, 777, 1)  # one chunk each
     # fp32 I/O: the chunk workspace also holds the fp16 K / Q rows
     f32base = 4 * (18 * (58368 + 32768 + 4) + 4 * 4)
-    assert tsa.gdn_chunked_workspace_bytes(1, 1100, 2, 4, f32=True) == \
-        (f32base + 255) // 256 * 256 + 4 * 4 * 3 * 65536 + rows(4, 1100, 5)
+    assert ws(1, 1100, 2, 4, f32=True, nseg=4) == (f32base + 255) // 256 * 256 + 4 * 4 * 3 * 65536 + rows(4, 1100, 5)
+    # invalid requests
+    lib = tsa.load()
+    assert lib.tsa_gdn_chunked_plan_workspace_bytes(1, 64, 1, 2, 128, 128, 64, 0, -1) == 0
+    assert lib.tsa_gdn_chunked_plan_workspace_bytes(1, 64, 1, 2, 128, 128, 64, 2, 0) == 0
+    assert lib.tsa_gdn_chunked_plan_workspace_bytes(1, 64, 1, 2, 128, 128, 32, 0, 0) == 0
+
+
+def test_gdn_plan_fwd_argument_errors():
+    # validated before any HIP call
+    lib = tsa.load()
+    f = lambda io=0, nseg=0, T=64, ws=DUMMY, wsb=1 << 30: lib.tsa_gdn_chunked_plan_fwd(
+        DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, T, 1, 2, 128, 128, 64, 0.1, io, nseg, ws, wsb, NULL)
+    assert f(io=2) == tsa.TSA_ERR_ARG
+    assert f(nseg=-1) == tsa.TSA_ERR_ARG
+    assert f(ws=NULL) == tsa.TSA_ERR_WORKSPACE
+    need = tsa.gdn_chunked_workspace_bytes(1, 1000, 1, 2, nseg=3)
+    assert f(T=1000, nseg=3, wsb=need - 1) == tsa.TSA_ERR_WORKSPACE
+    assert lib.tsa_gdn_chunked_plan_fwd(NULL, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 1, 2, 128, 128, 64,
+                                        0.1, 0, 0, DUMMY, 1 << 30, NULL) == tsa.TSA_ERR_NULL
 
 
 def test_gdn_noalloc_argument_errors():

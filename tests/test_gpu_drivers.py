@@ -16,6 +16,8 @@ BIN = os.path.join(ROOT, "turing-sm75_amd", "bin")
 ATTN_LINE = re.compile(r"^max \|(\w+)-naive\| : ([0-9.eE+-]+|nan|inf)\s+(OK|FAIL)\s*$")
 GDN_LINE = re.compile(r"^max \|(\w+)-naive\| : ([0-9.eE+-]+|nan|inf)\s+(OK|FAIL)\s+"
                       r"state rel ([0-9.eE+-]+|nan|inf)\s+(OK|FAIL)\s*$")
+# the chunk decomposition against the token-serial kernel (src/gdn_sm75.cu:1283-1289)
+CHUNK_SERIAL_LINE = re.compile(r"^max \|chunk-serial\| : ([0-9.eE+-]+|nan|inf)\s+(OK|FAIL)\s*$")
 
 
 def _run(argv, timeout=300):
@@ -64,8 +66,15 @@ def test_attn_driver(args):
 def test_gdn_driver(args):
     r = _run(["gdn"] + args)
     assert r.returncode == 0, (r.returncode, r.stderr)
-    checks = [GDN_LINE.match(l) for l in r.stdout.splitlines() if l.startswith("max |")]
+    lines = r.stdout.splitlines()
+    cs = [CHUNK_SERIAL_LINE.match(l) for l in lines if l.startswith("max |chunk-serial|")]
+    checks = [GDN_LINE.match(l) for l in lines if l.startswith("max |") and not l.startswith("max |chunk-serial|")]
     assert checks and all(checks), r.stdout
+    if "decode" in args:
+        assert not cs, r.stdout
+    else:  # printed once, before the per-kernel checks, as the reference does
+        assert len(cs) == 1 and cs[0] and lines.index(cs[0].group(0)) < lines.index(checks[0].group(0)), r.stdout
+        assert float(cs[0].group(1)) < 0.02 and cs[0].group(2) == "OK", cs[0].group(0)
     names = {m.group(1) for m in checks}
     assert names == ({"decode"} if "decode" in args else {"chunked", "recurrent"}), names
     for m in checks:

@@ -37,11 +37,11 @@ def _dev(dev, *arrays):
     return [torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in arrays]
 
 
-def _gpu(dev, kind, q, k, v, g, beta, st):
+def _gpu(dev, kind, q, k, v, g, beta, st, nseg=None):
     import torch
     tq, tk, tv, tg, tb, ts = _dev(dev, q, k, v, g, beta, st)
     if kind == "chunked":
-        o = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts)
+        o = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, nseg=nseg)
     elif kind == "recurrent":
         o = tsa.gdn_recurrent_fwd(tq, tk, tv, tg, tb, ts)
     else:
@@ -172,31 +172,26 @@ def test_ragged_and_head_map(dev, orc, kind, T):
 # The sequence split (few heads, many chunks): segments' transition maps run side by side with
 # their outputs, are combined (state after a segment = Phi state before + Z), and each chunk's
 # output is then fixed up in parallel (O = O_Z + M E).
-# TSA_GDN_SEGMENTS: None = the library's choice, "1" = no split, n = n segments.
+# segments: 0 = the library's plan, 1 = no split, n = n segments (tsa_gdn_chunked_plan_fwd).
 SPLIT_CASES = [
-    (1, 4096, 2, 4, None),   # 8 segments of 8 chunks (the library's choice for 4 heads)
-    (1, 2048, 8, 16, None),  # 16 heads: 2 segments of 16 chunks
-    (1, 1000, 1, 2, "3"),    # 6 + 6 + 4 chunks, the last chunk 40 tokens
-    (2, 777, 3, 4, "5"),     # 3 + 3 + 3 + 3 + 1 chunks, Hv % Hq != 0
-    (1, 200, 1, 2, "2"),     # 2 + 2 chunks, the last one 8 tokens
+    (1, 4096, 2, 4, 0),    # 8 segments of 8 chunks (the library's choice for 4 heads)
+    (1, 2048, 8, 16, 0),   # 16 heads: 2 segments of 16 chunks
+    (1, 1000, 1, 2, 3),    # 6 + 6 + 4 chunks, the last chunk 40 tokens
+    (2, 777, 3, 4, 5),     # 3 + 3 + 3 + 3 + 1 chunks, Hv % Hq != 0
+    (1, 200, 1, 2, 2),     # 2 + 2 chunks, the last one 8 tokens
 ]
 
 
-def _split_ws(monkeypatch, B, T, Hq, Hv, segs, f32=False):
+def _split_ws(B, T, Hq, Hv, segs, f32=False):
     """Workspace bytes with and without the split; the split's slots make the first larger,
     which shows the call takes the split."""
-    monkeypatch.setenv("TSA_GDN_SEGMENTS", "1")
-    plain = tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv, f32=f32)
-    if segs is None:
-        monkeypatch.delenv("TSA_GDN_SEGMENTS")
-    else:
-        monkeypatch.setenv("TSA_GDN_SEGMENTS", segs)
-    return tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv, f32=f32), plain
+    plain = tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv, f32=f32, nseg=1)
+    return tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv, f32=f32, nseg=segs), plain
 
 
 @pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "B{}T{}Hq{}Hv{}s{}".format(*c))
 @pytest.mark.parametrize("decay", ["fast", "slow"])
-def test_sequence_split(dev, orc, monkeypatch, case, decay):
+def test_sequence_split(dev, orc, case, decay):
     """Against the oracle, entering with an N(0, 0.02) state.  With the slow gate (about
     -0.002 per token) the state entering a segment still weighs at its end, so the maps and
     their combine decide the result; the plain carry on the same inputs passes the same gates."""
@@ -205,25 +200,26 @@ def test_sequence_split(dev, orc, monkeypatch, case, decay):
     q, k, v, g, beta, st = _inputs(rng, B, T, Hq, Hv, sstd=0.02)
     if decay == "slow":
         g = (-0.002 * (1 + 0.5 * rng.standard_normal(g.shape))).astype(np.float32)
-    need, plain = _split_ws(monkeypatch, B, T, Hq, Hv, segs)
+    need, plain = _split_ws(B, T, Hq, Hv, segs)
     print(f"split B={B} T={T} Hq={Hq} Hv={Hv} segments={segs} ws {need} (plain {plain})", flush=True)
     assert need > plain
-    o, s = _gpu(dev, "chunked", q, k, v, g, beta, st)
+    if segs == 0:  # the library's plan is the default call's
+        assert need == tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv)
+    o, s = _gpu(dev, "chunked", q, k, v, g, beta, st, nseg=segs)
     o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
     _check(o, s, o_ref, s_ref, *TOL["chunked"], label=f"split {decay}")
-    monkeypatch.setenv("TSA_GDN_SEGMENTS", "1")
-    o1, s1 = _gpu(dev, "chunked", q, k, v, g, beta, st)
+    o1, s1 = _gpu(dev, "chunked", q, k, v, g, beta, st, nseg=1)
     _check(o1, s1, o_ref, s_ref, *TOL["chunked"], label=f"plain {decay}")
 
 
-def test_sequence_split_fp32_io(dev, orc, monkeypatch):
+def test_sequence_split_fp32_io(dev, orc):
     """The split with fp32 I/O (K / Q rows from the prep's fp16 copies in the workspace):
     2 segments of 9 chunks."""
     rng = np.random.default_rng(411)
     B, T, Hq, Hv = 1, 1100, 2, 4
     q, k, v, g, beta, st = (a.astype(np.float32) for a in _inputs(rng, B, T, Hq, Hv, sstd=0.02))
     g = (-0.002 * (1 + 0.5 * rng.standard_normal(g.shape))).astype(np.float32)
-    need, plain = _split_ws(monkeypatch, B, T, Hq, Hv, None, f32=True)
+    need, plain = _split_ws(B, T, Hq, Hv, 0, f32=True)
     print(f"split fp32 I/O ws {need} (plain {plain})", flush=True)
     assert need > plain
     o, s = _gpu(dev, "chunked", q, k, v, g, beta, st)
@@ -231,14 +227,14 @@ def test_sequence_split_fp32_io(dev, orc, monkeypatch):
     _check(o, s, o_ref, s_ref, 2e-3, 8e-4, label="split fp32 I/O")
 
 
-def test_sequence_split_workspace_contents_do_not_matter(dev, monkeypatch):
+def test_sequence_split_workspace_contents_do_not_matter(dev):
     """Every slot of the split is written before it is read: a workspace of 0xff bytes gives
     the same results bit for bit as a zeroed one."""
     import torch
     rng = np.random.default_rng(412)
     B, T, Hq, Hv = 1, 2048, 2, 4
     q, k, v, g, beta, st = _inputs(rng, B, T, Hq, Hv, sstd=0.02)
-    need, plain = _split_ws(monkeypatch, B, T, Hq, Hv, None)
+    need, plain = _split_ws(B, T, Hq, Hv, 0)
     assert need > plain
     tq, tk, tv, tg, tb = _dev(dev, q, k, v, g, beta)
     ws = torch.zeros(need, dtype=torch.uint8, device=dev)
@@ -333,20 +329,40 @@ def test_workspace_too_small_raises(dev):
     assert e.value.code == tsa.TSA_ERR_WORKSPACE
 
 
-def test_chunked_carry_gives_up_and_is_redone(dev, orc, monkeypatch):
-    """Beside the prep, a carry workgroup that finds a chunk not ready gives up (wait limit 0
-    through TSA_GDN_CARRY_WAIT_US), leaves its state columns alone, and the second carry launch
-    after the prep redoes it.  Whatever mix of workgroups gives up, the results equal the
-    default run bit for bit and the oracle within the gates."""
+def _as(io, *arrays):
+    return arrays if io == "f16" else tuple(a.astype(np.float32) for a in arrays)
+
+
+@pytest.mark.parametrize("io", ["f16", "f32"])
+def test_chunked_carry_gives_up_and_is_redone(dev, orc, monkeypatch, io):
+    """With the overlap asked for (TSA_GDN_OVERLAP=1), a carry workgroup beside the prep that
+    finds a chunk not ready gives up (wait limit 0 through TSA_GDN_CARRY_WAIT_US), leaves its
+    state columns alone, and the second carry launch after the prep redoes it, overwriting
+    the output rows it had written (fp32 I/O: the K / Q rows come from the prep's fp16 copies
+    in the workspace).  Whatever mix of workgroups gives up, the results equal the default
+    in-order run bit for bit and the oracle within the gates."""
+    import torch
     rng = np.random.default_rng(402)
-    q, k, v, g, beta, st = _inputs(rng, 1, 1024, 16, 32, sstd=0.02)
+    B, T, Hq, Hv = 1, 1024, 16, 32
+    q, k, v, g, beta, st = _inputs(rng, B, T, Hq, Hv, sstd=0.02)
+    q, k, v = _as(io, q, k, v)
     o0, s0 = _gpu(dev, "chunked", q, k, v, g, beta, st)
+    monkeypatch.setenv("TSA_GDN_OVERLAP", "1")
     monkeypatch.setenv("TSA_GDN_CARRY_WAIT_US", "0")
+    f32 = io == "f32"
+    ws = torch.zeros(tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv, f32=f32), dtype=torch.uint8, device=dev)
+    redone = []
     for _ in range(3):
-        o1, s1 = _gpu(dev, "chunked", q, k, v, g, beta, st)
+        tq, tk, tv, tg, tb, ts = _dev(dev, q, k, v, g, beta, st)
+        o1 = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, ws=ws).float().cpu().numpy()
+        s1 = ts.cpu().numpy()
         assert np.array_equal(o1, o0) and np.array_equal(s1, s0)
+        redone.append(tsa.gdn_chunked_redo_count(ws, B, T, Hq, Hv, f32=f32))
+    print(f"{io}: carry workgroups redone per call {redone}")
+    assert all(0 <= n <= B * Hv * 4 for n in redone)
     o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
-    _check(o1, s1, o_ref, s_ref, *TOL["chunked"], label="chunked, carry waits limited to 0")
+    tol = TOL["chunked"] if io == "f16" else (2e-3, 8e-4)
+    _check(o1, s1, o_ref, s_ref, *tol, label=f"chunked {io}, overlap, carry waits limited to 0")
 
 
 def _ws_fill(ws, kind):
@@ -361,20 +377,26 @@ def _ws_fill(ws, kind):
         ws.copy_(torch.randint(0, 256, ws.shape, generator=g, device=ws.device, dtype=torch.uint8))
 
 
-@pytest.mark.parametrize("wait_us", [None, "0"])
-def test_chunked_workspace_contents_do_not_matter(dev, monkeypatch, wait_us):
-    """Each call clears its own ready flags and abort words before its kernels read them, so a
-    workspace holding any bytes -- in particular flags that already read as published --
-    gives results bit-identical to a zeroed one, with the overlap working normally and with
-    every carry wait cut to zero."""
+@pytest.mark.parametrize("io", ["f16", "f32"])
+@pytest.mark.parametrize("mode", ["in_order", "overlap", "overlap_wait0"])
+def test_chunked_workspace_contents_do_not_matter(dev, monkeypatch, mode, io):
+    """A workspace holding any bytes -- in particular flags that already read as published and
+    abort words that read as "redo" -- gives results bit-identical to a zeroed one: in order
+    (the default) the prep sets every flag before the carry reads it and the carry zeroes the
+    abort words; with the overlap the call clears both first, with the overlap working
+    normally and with every carry wait cut to zero."""
     import torch
-    if wait_us is not None:
-        monkeypatch.setenv("TSA_GDN_CARRY_WAIT_US", wait_us)
+    if mode != "in_order":
+        monkeypatch.setenv("TSA_GDN_OVERLAP", "1")
+    if mode == "overlap_wait0":
+        monkeypatch.setenv("TSA_GDN_CARRY_WAIT_US", "0")
     rng = np.random.default_rng(406)
     B, T, Hq, Hv = 1, 1024, 16, 32
     q, k, v, g, beta, st = _inputs(rng, B, T, Hq, Hv, sstd=0.02)
+    q, k, v = _as(io, q, k, v)
+    f32 = io == "f32"
     tq, tk, tv, tg, tb = _dev(dev, q, k, v, g, beta)
-    need = tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv)
+    need = tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv, f32=f32)
     assert need % 4 == 0
     ws = torch.zeros(need, dtype=torch.uint8, device=dev)
     ts = _dev(dev, st)[0]
@@ -386,27 +408,30 @@ def test_chunked_workspace_contents_do_not_matter(dev, monkeypatch, wait_us):
         o1 = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, ws=ws)
         torch.cuda.synchronize()
         assert torch.equal(o1, o0) and torch.equal(ts, s0), kind
-        n = tsa.gdn_chunked_redo_count(ws, B, T, Hq, Hv)
-        print(f"workspace {kind}: redone carry workgroups {n}")
+        n = tsa.gdn_chunked_redo_count(ws, B, T, Hq, Hv, f32=f32)
+        print(f"{mode} {io} workspace {kind}: redone carry workgroups {n}")
         assert 0 <= n <= B * Hv * 4
+        if mode == "in_order":
+            assert n == 0
 
 
-def test_chunked_in_order_opt_out(dev, monkeypatch):
-    """TSA_GDN_OVERLAP=0 runs the prep and the carry in order on the caller's stream: the same
-    results bit for bit, and no carry workgroup is ever redone."""
+def test_chunked_overlap_opt_in(dev, monkeypatch):
+    """In order on the caller's stream is the default; TSA_GDN_OVERLAP=1 runs the prep beside
+    the carry: the same results bit for bit either way, and in order no carry workgroup is
+    ever redone, whatever the workspace held."""
     import torch
     rng = np.random.default_rng(407)
     B, T, Hq, Hv = 2, 500, 4, 8
     q, k, v, g, beta, st = _inputs(rng, B, T, Hq, Hv, sstd=0.02)
-    o0, s0 = _gpu(dev, "chunked", q, k, v, g, beta, st)
-    monkeypatch.setenv("TSA_GDN_OVERLAP", "0")
     tq, tk, tv, tg, tb, ts = _dev(dev, q, k, v, g, beta, st)
     ws = torch.empty(tsa.gdn_chunked_workspace_bytes(B, T, Hq, Hv), dtype=torch.uint8, device=dev)
     _ws_fill(ws, "ones")
-    o1 = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, ws=ws)
-    torch.cuda.synchronize()
-    assert np.array_equal(o1.float().cpu().numpy(), o0) and np.array_equal(ts.cpu().numpy(), s0)
+    o0 = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, ws=ws).float().cpu().numpy()
+    s0 = ts.cpu().numpy()
     assert tsa.gdn_chunked_redo_count(ws, B, T, Hq, Hv) == 0
+    monkeypatch.setenv("TSA_GDN_OVERLAP", "1")
+    o1, s1 = _gpu(dev, "chunked", q, k, v, g, beta, st)
+    assert np.array_equal(o1, o0) and np.array_equal(s1, s0)
 
 
 def test_wrong_out_shape_raises_before_launch(dev):
@@ -448,14 +473,15 @@ sys.exit(0 if (eo < 2e-3 and es < 3e-4) else 1)
 
 
 def test_chunked_under_serialised_dispatch(dev):
-    """With every dispatch serialised (AMD_SERIALIZE_KERNEL=3, as under a profiler that
-    collects counters), the carry launched beside the prep cannot see it run; it must give up,
-    and the second launch must still produce the correct result (one child process)."""
+    """With the overlap asked for (TSA_GDN_OVERLAP=1) and every dispatch serialised
+    (AMD_SERIALIZE_KERNEL=3, as under a profiler that collects counters), the carry launched
+    beside the prep cannot see it run; it must give up, and the second launch must still
+    produce the correct result (one child process)."""
     import os
     import subprocess
     import sys
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    env = dict(os.environ, AMD_SERIALIZE_KERNEL="3")
+    env = dict(os.environ, AMD_SERIALIZE_KERNEL="3", TSA_GDN_OVERLAP="1")
     r = subprocess.run([sys.executable, "-c", _SERIAL_CHILD, root, os.path.join(root, "turing-sm75_amd")],
                        env=env, capture_output=True, text=True, timeout=240)
     print(r.stdout[-2000:], r.stderr[-2000:])
@@ -471,7 +497,6 @@ def test_chunked_under_graph_capture(dev, monkeypatch, shape):
     entry point."""
     import ctypes
     import torch
-    monkeypatch.delenv("TSA_GDN_SEGMENTS", raising=False)
     B, T, Hq, Hv = shape
     print(f"graph capture B={B} T={T} Hq={Hq} Hv={Hv}", flush=True)
     rng = np.random.default_rng(T + Hv)

@@ -51,13 +51,9 @@ def _inputs(rng, B, T, Hq, Hv, slow):
 
 @pytest.mark.parametrize("case", _cases(), ids=lambda c: "c{}_B{}T{}Hq{}Hv{}{}{}s{}".format(
     c[0], c[1], c[2], c[3], c[4], "_f32" if c[5] else "", "_slow" if c[6] else "", c[7]))
-def test_shape_sweep(dev, orc, monkeypatch, case):
+def test_shape_sweep(dev, orc, case):
     import torch
     i, B, T, Hq, Hv, f32, slow, segs = case
-    if segs is None:
-        monkeypatch.delenv("TSA_GDN_SEGMENTS", raising=False)
-    else:
-        monkeypatch.setenv("TSA_GDN_SEGMENTS", segs)
     print(f"sweep case {i}: B={B} T={T} Hq={Hq} Hv={Hv} f32={f32} slow={slow} segments={segs}", flush=True)
     rng = np.random.default_rng(1000 + i)
     arrays = _inputs(rng, B, T, Hq, Hv, slow)
@@ -67,8 +63,10 @@ def test_shape_sweep(dev, orc, monkeypatch, case):
     scale = float(np.abs(s_ref).max())
     for kind in ("chunked", "recurrent"):
         tq, tk, tv, tg, tb, ts = (torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in arrays)
-        fn = tsa.gdn_chunked_fwd if kind == "chunked" else tsa.gdn_recurrent_fwd
-        o = fn(tq, tk, tv, tg, tb, ts)
+        if kind == "chunked":
+            o = tsa.gdn_chunked_fwd(tq, tk, tv, tg, tb, ts, nseg=None if segs is None else int(segs))
+        else:
+            o = tsa.gdn_recurrent_fwd(tq, tk, tv, tg, tb, ts)
         torch.cuda.synchronize()
         assert o.dtype == (torch.float32 if f32 else torch.float16)
         eo = float(np.abs(o.float().cpu().numpy() - o_ref).max())

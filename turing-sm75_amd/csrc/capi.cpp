@@ -125,22 +125,40 @@ extern "C" size_t tsa_gdn_chunked_workspace_bytes_f32(int B, int T, int Hq, int 
     return tsa::gdn_chunked_ws_bytes(B, T, Hv, true);
 }
 
+extern "C" size_t tsa_gdn_chunked_plan_workspace_bytes(int B, int T, int Hq, int Hv, int dk, int dv,
+                                                       int chunk, int io_f32, int nseg) {
+    if (B < 1 || T < 1 || Hq < 1 || Hv < 1 || dk != 128 || dv != 128 || chunk != 64) return 0;
+    if ((io_f32 != 0 && io_f32 != 1) || nseg < 0) return 0;
+    return tsa::gdn_chunked_ws_bytes(B, T, Hv, io_f32 != 0, nseg);
+}
+
 namespace {
 int chunked(const void* q, const void* k, const void* v, const float* g_log, const float* beta,
             float* state, void* out, int B, int T, int Hq, int Hv, int dk, int dv, int chunk,
-            float scale, void* ws, size_t ws_bytes, bool f32, void* stream) {
+            float scale, void* ws, size_t ws_bytes, bool f32, void* stream, int nseg = 0) {
     int rc = check_gdn(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, scale);
     if (rc) return rc;
     if (chunk < 1) return TSA_ERR_SHAPE;
     if (dk != 128 || dv != 128 || chunk != 64) return TSA_ERR_UNSUPPORTED;
+    if (nseg < 0) return TSA_ERR_ARG;
     const long long nch = (T + 63LL) / 64;
     if (!fits_int(B, Hv, nch) || !fits_int(B, Hv, 8)) return TSA_ERR_SHAPE;
-    const size_t need = tsa::gdn_chunked_ws_bytes(B, T, Hv, f32);
+    const size_t need = tsa::gdn_chunked_ws_bytes(B, T, Hv, f32, nseg);
     if (!ws || ws_bytes < need) return TSA_ERR_WORKSPACE;
     return from_hip(tsa::gdn_chunked(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, scale, ws, f32,
-                                     as_stream(stream)));
+                                     as_stream(stream), nseg));
 }
 }  // namespace
+
+extern "C" int tsa_gdn_chunked_plan_fwd(const void* q, const void* k, const void* v,
+                                        const float* g_log, const float* beta, float* state, void* out,
+                                        int B, int T, int Hq, int Hv, int dk, int dv, int chunk,
+                                        float scale, int io_f32, int nseg, void* ws, size_t ws_bytes,
+                                        void* stream) {
+    if (io_f32 != 0 && io_f32 != 1) return TSA_ERR_ARG;
+    return chunked(q, k, v, g_log, beta, state, out, B, T, Hq, Hv, dk, dv, chunk, scale, ws, ws_bytes,
+                   io_f32 != 0, stream, nseg);
+}
 
 extern "C" int tsa_gdn_chunked_fwd(const void* q, const void* k, const void* v,
                                    const float* g_log, const float* beta, float* state, void* out,

@@ -218,8 +218,11 @@ struct PrepLds {
 // and g_log / beta are computed from the raw projections a / b (gate arguments).
 // TIO: the q / k / v element type (fp16, or fp32 with the K / Q rows left in fp16 in the
 // workspace for the carry).
+// Four workgroups per CU (128 VGPRs); the fp32-I/O form holds its fp32 loads before converting
+// them and needs more registers, so it runs three per CU rather than spill.
+template <typename TIO> constexpr int prep_wgs_per_cu() { return std::is_same<TIO, float>::value ? 3 : 4; }
 template <bool kFused, typename TIO>
-__global__ void __launch_bounds__(kThreads, 4)
+__global__ void __launch_bounds__(kThreads, prep_wgs_per_cu<TIO>())
 gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
                const TIO* __restrict__ v, const float* __restrict__ g_log,
                const float* __restrict__ beta, GdnRawGates gates, unsigned char* __restrict__ ws,
@@ -1302,23 +1305,22 @@ long env_long(const char* name, long def, long hi) {
 // The sequence split of a call: nseg segments of seg_len chunks (nseg == 1: no split).  It pays
 // where the carry's workgroups leave most CUs idle (few heads) and the chunk chain is long.
 // The call's serial time is about nch / nseg chunk steps (the maps) + nseg - 1 combine steps
-// (each about a chunk step) + the fixup, least near nseg = sqrt(nch); the plan takes the most
-// segments up to sqrt(nch) whose maps launch ((2 nseg - 1) units of 4 workgroups per head)
-// fits in the 256 CUs of the part, each at least kMinSegChunks chunks long.  TSA_GDN_SEGMENTS
-// overrides the choice: 1 never splits, n >= 2 asks for n segments (fewer if the sequence has
-// fewer chunks).  The workspace size follows the plan, so a caller sizes the workspace with
-// the same setting it calls with (the entry points check the size they are given).
+// (each about a chunk step) + the fixup, least near nseg = sqrt(nch); the library's plan
+// (req = 0) takes the most segments up to sqrt(nch) whose maps launch ((2 nseg - 1) units of 4
+// workgroups per head) fits in the 256 CUs of the part, each at least kMinSegChunks chunks
+// long: a function of the shapes only, so a workspace sized once serves every call of a shape.
+// An explicit request (tsa_gdn_chunked_plan_fwd) replaces it: req = 1 never splits, req >= 2
+// asks for req segments (fewer if the sequence has fewer chunks: no segment is empty).
 constexpr int kSplitCUs = 256;
 constexpr int kMinSegChunks = 8;
 struct SegPlan {
     int nseg = 1, seg_len = 0;
 };
-SegPlan seg_plan(int BHv, int nch) {
-    const long forced = env_long("TSA_GDN_SEGMENTS", 0, 1 << 20);
+SegPlan seg_plan(int BHv, int nch, int req) {
     long n = 1;
-    if (forced >= 2)
-        n = std::min<long>(forced, nch);
-    else if (forced == 0 && BHv > 0)
+    if (req >= 2)
+        n = std::min<long>(req, nch);
+    else if (req == 0 && BHv > 0)
         n = std::min<long>(std::min<long>((kSplitCUs / (4 * BHv) + 1) / 2, nch / kMinSegChunks),
                            (long)std::sqrt((double)nch));
     if (n < 2) return {};
@@ -1352,25 +1354,25 @@ size_t ws_bytes_for(size_t BHv, size_t nch, int T, bool f32, const SegPlan& plan
 
 // The plan of a call whose workspace holds at most `budget` bytes: the split where it fits,
 // else none (the no-allocation entry's fixed scratch).
-SegPlan call_plan(int BHv, int nch, int T, bool f32, size_t budget) {
-    SegPlan plan = seg_plan(BHv, nch);
+SegPlan call_plan(int BHv, int nch, int T, bool f32, size_t budget, int req) {
+    SegPlan plan = seg_plan(BHv, nch, req);
     if (plan.nseg > 1 && ws_bytes_for((size_t)BHv, (size_t)nch, T, f32, plan) > budget) plan = SegPlan{};
     return plan;
 }
 }  // namespace
 
-size_t gdn_chunked_ws_bytes(int B, int T, int Hv, bool f32) {
+size_t gdn_chunked_ws_bytes(int B, int T, int Hv, bool f32, int nseg) {
     const int nch = (T + kC - 1) / kC, BHv = B * Hv;
-    return ws_bytes_for((size_t)BHv, (size_t)nch, T, f32, call_plan(BHv, nch, T, f32, SIZE_MAX));
+    return ws_bytes_for((size_t)BHv, (size_t)nch, T, f32, call_plan(BHv, nch, T, f32, SIZE_MAX, nseg));
 }
 
 namespace {
 
-// The prep runs on a second stream of the device so that it overlaps the carry: the carry
-// copies a chunk's operands as soon as the prep has published them (ready flags), and the
-// chunk-major prep order produces them in the order the carry consumes them.  One side
-// stream and its fork / join events per device, created on the first call that overlaps on
-// that device and kept until the process ends (the library's only process-wide state).
+// With TSA_GDN_OVERLAP=1 the prep runs on a second stream of the device so that it overlaps
+// the carry: the carry copies a chunk's operands as soon as the prep has published them
+// (ready flags), and the chunk-major prep order produces them in the order the carry consumes
+// them.  One side stream and its fork / join events per device, created on the first call
+// that overlaps on that device and kept until the process ends.
 struct SideStream {
     bool tried = false, ok = false;
     int cus = 0;
@@ -1384,16 +1386,17 @@ SideStream g_side[kMaxDevices];
 // Longest wait of a carry workgroup for a chunk, in ticks of the 100 MHz real-time counter.
 unsigned carry_wait_ticks() { return (unsigned)(env_long("TSA_GDN_CARRY_WAIT_US", 2000, 10000000) * 100); }
 
-// TSA_GDN_OVERLAP=0 runs the prep and the carry in order on the caller's stream (no side
-// stream): for schedulers that cannot run the two kernels side by side, where every call
-// would otherwise wait out the carry's time limit before its second launch.
-bool overlap_allowed() { return env_long("TSA_GDN_OVERLAP", 1, 1) != 0; }
+// The prep and the carry run in order on the caller's stream unless the environment variable
+// TSA_GDN_OVERLAP=1 asks for the side-by-side form (the prep on a second stream, the carry
+// waiting on its ready flags).  In order is the default: at 32 heads it measured as fast as
+// the overlap, and it needs no side stream, events, mutex, flag clear or second carry launch.
+bool overlap_requested() { return env_long("TSA_GDN_OVERLAP", 0, 1) != 0; }
 
 template <bool kFused, typename TIO>
 hipError_t launch_chunked(const void* q, const void* k, const void* v, const float* g_log,
                           const float* beta, const GdnRawGates& gates, float* state, void* out,
                           int B, int T, int Hq, int Hv, float scale, void* ws, bool may_overlap,
-                          hipStream_t stream, size_t ws_budget = SIZE_MAX) {
+                          hipStream_t stream, size_t ws_budget = SIZE_MAX, int nseg = 0) {
     const int nch = (T + kC - 1) / kC;
     const int BHv = B * Hv;
     const int carry_wgs = BHv * (kD / (16 * kStrips));
@@ -1422,7 +1425,7 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
     };
 
     // Sequence split: in order on the caller's stream (the maps need every chunk's operands)
-    const SegPlan plan = call_plan(BHv, nch, T, std::is_same<TIO, float>::value, ws_budget);
+    const SegPlan plan = call_plan(BHv, nch, T, std::is_same<TIO, float>::value, ws_budget, nseg);
     if (plan.nseg > 1) {
         CarryJob job;
         job.phase = kJobMaps;
@@ -1452,16 +1455,17 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
         return e;
     }
 
-    // Overlap only when it cannot stall: the carry's workgroups (one per CU) must leave at
-    // least half the CUs to the prep, and a stream being captured into a graph runs the two
-    // kernels in order (a graph does not promise to run sibling nodes concurrently).
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
-    // The side stream belongs to the device of the caller's stream (the null stream: the
-    // current device), which need not be the current device.
+    // The default, and every call that cannot overlap: in order on the caller's stream, with no
+    // other runtime call.  The overlap (TSA_GDN_OVERLAP=1) is taken only when it cannot stall:
+    // the carry's workgroups (one per CU) must leave at least half the CUs to the prep, and a
+    // stream being captured into a graph runs the two kernels in order (a graph does not promise
+    // to run sibling nodes concurrently).  The side stream belongs to the device of the caller's
+    // stream (the null stream: the current device), which need not be the current device.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusActive;
     int dev = -1;
     SideStream* side = nullptr;
-    if (may_overlap && nch > 1 && cap == hipStreamCaptureStatusNone && overlap_allowed() &&
+    if (may_overlap && nch > 1 && overlap_requested() && hipStreamIsCapturing(stream, &cap) == hipSuccess &&
+        cap == hipStreamCaptureStatusNone &&
         (stream ? hipStreamGetDevice(stream, &dev) == hipSuccess : hipGetDevice(&dev) == hipSuccess) &&
         dev >= 0 && dev < kMaxDevices) {
         std::lock_guard<std::mutex> lock(g_side_mu);
@@ -1547,7 +1551,7 @@ size_t gdn_chunked_noalloc_max_bytes() { return kScratchBytes; }
 // The no-allocation entry splits the sequence only where the split's workspace fits the scratch.
 size_t gdn_chunked_noalloc_ws_bytes(int B, int T, int Hv) {
     const int nch = (T + kC - 1) / kC, BHv = B * Hv;
-    return ws_bytes_for((size_t)BHv, (size_t)nch, T, false, call_plan(BHv, nch, T, false, kScratchBytes));
+    return ws_bytes_for((size_t)BHv, (size_t)nch, T, false, call_plan(BHv, nch, T, false, kScratchBytes, 0));
 }
 
 hipError_t gdn_chunked_noalloc(const void* q, const void* k, const void* v, const float* g_log,
@@ -1582,12 +1586,12 @@ hipError_t gdn_chunked_redo_count(const void* ws, int B, int T, int Hv, bool f32
 
 hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,
                        const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
-                       float scale, void* ws, bool f32, hipStream_t stream) {
+                       float scale, void* ws, bool f32, hipStream_t stream, int nseg) {
     if (f32)
         return launch_chunked<false, float>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq,
-                                            Hv, scale, ws, true, stream);
+                                            Hv, scale, ws, true, stream, SIZE_MAX, nseg);
     return launch_chunked<false, half_t>(q, k, v, g_log, beta, GdnRawGates{}, state, out, B, T, Hq, Hv,
-                                         scale, ws, true, stream);
+                                         scale, ws, true, stream, SIZE_MAX, nseg);
 }
 
 hipError_t gdn_chunked_fused(const void* q, const void* k, const void* v, const GdnRawGates& gates,

@@ -28,10 +28,12 @@ struct GdnRawGates {
 };
 
 // f32: q / k / v / out are fp32 (the reference's own I/O; a larger workspace), else fp16.
-size_t gdn_chunked_ws_bytes(int B, int T, int Hv, bool f32 = false);
+// nseg: the sequence-split plan, 0 = the library's (a function of the shapes), 1 = no split,
+// n >= 2 = n segments (fewer when the sequence has fewer chunks).
+size_t gdn_chunked_ws_bytes(int B, int T, int Hv, bool f32 = false, int nseg = 0);
 hipError_t gdn_chunked(const void* q, const void* k, const void* v, const float* g_log,
                        const float* beta, float* state, void* out, int B, int T, int Hq, int Hv,
-                       float scale, void* ws, bool f32, hipStream_t stream);
+                       float scale, void* ws, bool f32, hipStream_t stream, int nseg = 0);
 // The chunked prefill without a caller workspace: the library's fixed device scratch array
 // (gdn_chunked_noalloc_max_bytes() bytes per GPU) stands in for it; no allocation, no side
 // stream.  The caller checks gdn_chunked_ws_bytes(...) against the maximum.

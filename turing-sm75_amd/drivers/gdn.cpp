@@ -5,8 +5,9 @@
 //
 // Mirrors main() of src/gdn_sm75.cu:1246-1412: T (default 64), shape d = 128, Hq = 16,
 // Hv = 48, scale 1/sqrt(128), the reference's LCG inputs (--dist lcg, :1270-1279), state
-// zero, every kernel checked against the naive kernel (max |out - naive| < 0.02, plus the
-// fp32 state within 1e-3 relative), state reset before each checked launch (:1316), 20 timed
+// zero, the chunked output first compared with the token-serial one (max |chunk-serial|,
+// :1283-1289), then every kernel checked against the naive kernel (max |out - naive| < 0.02,
+// plus the fp32 state within 1e-3 relative), state reset before each checked launch (:1316), 20 timed
 // launches, "ms x48 layers" (:1331).  --io f32 (the default with the LCG inputs) runs q / k /
 // v / out in fp32 through the *_f32 entry points, the reference's own precision (:57-64);
 // --io f16 (the default with --dist normal) rounds them to fp16, the library's I/O type.
@@ -180,6 +181,23 @@ int run(const Shape& sh) {
             DRV_TSA(Api<E>::recurrent(q.d, k.d, v.d, g.d, b.d, st.d, o.d, B, T, Hq, Hv, d, d, scale, nullptr));
         };
         const double tokens = (double)B * T;
+        // the chunk decomposition against the token-serial recurrence, as the reference
+        // compares gdn_chunked_cpu with gdn_cpu before it checks its GPU kernels
+        // (src/gdn_sm75.cu:1283-1289); here both are the library's kernels on the device
+        {
+            std::vector<E> o_ch, o_se;
+            st.upload(in.st);
+            chunked();
+            DRV_HIP(hipDeviceSynchronize());
+            o.download(o_ch);
+            st.upload(in.st);
+            recurrent();
+            DRV_HIP(hipDeviceSynchronize());
+            o.download(o_se);
+            const float ecs = max_abs(o_ch, o_se);
+            worst_out = std::max(worst_out, ecs);
+            std::printf("max |chunk-serial| : %.5f   %s\n", ecs, ecs < 2e-2f ? "OK" : "FAIL");
+        }
         for (auto kv : {std::make_pair("chunked", 0), std::make_pair("recurrent", 1)}) {
             st.upload(in.st);
             if (kv.second == 0) chunked(); else recurrent();

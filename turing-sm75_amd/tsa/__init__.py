@@ -59,6 +59,8 @@ _SIGNATURES = {
     "tsa_gdn_chunked_fwd_noalloc": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp]),
     "tsa_gdn_chunked_redo_count": (_i, [_vp, _sz] + [_i] * 8 + [ctypes.POINTER(ctypes.c_int), _vp]),
     "tsa_gdn_chunked_workspace_bytes_f32": (_sz, [_i] * 7),
+    "tsa_gdn_chunked_plan_workspace_bytes": (_sz, [_i] * 9),
+    "tsa_gdn_chunked_plan_fwd": (_i, [_vp] * 7 + [_i] * 7 + [_f, _i, _i, _vp, _sz, _vp]),
     "tsa_gdn_chunked_fwd_f32": (_i, [_vp] * 7 + [_i] * 7 + [_f, _vp, _sz, _vp]),
     "tsa_gdn_recurrent_fwd_f32": (_i, [_vp] * 7 + [_i] * 6 + [_f, _vp]),
     "tsa_gdn_decode_step_f32": (_i, [_vp] * 7 + [_i] * 5 + [_f, _vp]),
@@ -249,34 +251,41 @@ def _gdn_shapes(q, k, v, g_log, beta, state, batched_t: bool):
     return B, T, Hq, Hv, dk, dv
 
 
-def gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk=128, dv=128, chunk=64, f32=False) -> int:
-    """Workspace bytes of one chunked call.  With few heads and many chunks the call splits the
-    sequence and needs more (TSA_GDN_SEGMENTS, read at each query and call, overrides the
-    plan: query under the setting the call will see)."""
+def gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk=128, dv=128, chunk=64, f32=False, nseg=None) -> int:
+    """Workspace bytes of one chunked call.  With few heads and many chunks the library's plan
+    splits the sequence and needs more; the plan is a function of the shapes.  nseg asks for
+    an explicit plan (0 = the library's, 1 = no split, n >= 2 = n segments)."""
+    if nseg is not None:
+        return int(load().tsa_gdn_chunked_plan_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk, int(bool(f32)),
+                                                               int(nseg)))
     fn = load().tsa_gdn_chunked_workspace_bytes_f32 if f32 else load().tsa_gdn_chunked_workspace_bytes
     return int(fn(B, T, Hq, Hv, dk, dv, chunk))
 
 
 def gdn_chunked_fwd(q, k, v, g_log, beta, state, out=None, scale=None, chunk=64, ws=None,
-                    stream=None):
+                    stream=None, nseg=None):
     """Chunked prefill; state [B, Hv, dv, dk] is updated in place; returns out.  fp32 q/k/v
     select tsa_gdn_chunked_fwd_f32 (fp32 out).  With few heads (B*Hv <= 21) and at least 16
     chunks the library splits the sequence into segments run side by side (same results to
-    fp32 rounding)."""
+    fp32 rounding).  nseg (through tsa_gdn_chunked_plan_fwd) asks for an explicit plan: 0 =
+    the library's, 1 = no split, n >= 2 = n segments."""
     import torch
     B, T, Hq, Hv, dk, dv = _gdn_shapes(q, k, v, g_log, beta, state, True)
     out = _out(out, v)
     if scale is None:
         scale = 1.0 / math.sqrt(dk)
     f32 = q.dtype == torch.float32
-    need = gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk, f32=f32)
+    need = gdn_chunked_workspace_bytes(B, T, Hq, Hv, dk, dv, chunk, f32=f32, nseg=nseg)
     if ws is None:
         ws = _scratch(need, q.device, stream)
-    fn = load().tsa_gdn_chunked_fwd_f32 if f32 else load().tsa_gdn_chunked_fwd
-    _check(fn(
-        _ptr(q), _ptr(k), _ptr(v), _ptr(g_log), _ptr(beta), _ptr(state), _ptr(out),
-        B, T, Hq, Hv, dk, dv, chunk, float(scale), _ptr(ws), ws.numel() * ws.element_size(),
-        _stream(stream)))
+    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(g_log), _ptr(beta), _ptr(state), _ptr(out),
+            B, T, Hq, Hv, dk, dv, chunk, float(scale))
+    tail = (_ptr(ws), ws.numel() * ws.element_size(), _stream(stream))
+    if nseg is not None:
+        _check(load().tsa_gdn_chunked_plan_fwd(*args, int(f32), int(nseg), *tail))
+    else:
+        fn = load().tsa_gdn_chunked_fwd_f32 if f32 else load().tsa_gdn_chunked_fwd
+        _check(fn(*args, *tail))
     return out
 
 
