@@ -105,7 +105,7 @@ def test_gdn_f32_entry_points_validate_like_fp16():
     lib = tsa.load()
     args = [DUMMY] * 7
     need32 = tsa.gdn_chunked_workspace_bytes(1, 100, 2, 4, f32=True)
-    assert need32 == tsa.gdn_chunked_workspace_bytes(1, 100, 2, 4) + 2 * 32768 * 4  # + K, Q rows
+    assert need32 == tsa.gdn_chunked_workspace_bytes(1, 100, 2, 4) + 2 * 49152 * 4  # + K, Q, K_lo rows
     ch = lambda ws=DUMMY, nb=need32, dk=128, T=100: lib.tsa_gdn_chunked_fwd_f32(
         *args, 1, T, 2, 4, dk, 128, 64, 0.1, ws, nb, NULL)
     assert ch(ws=NULL) == tsa.TSA_ERR_WORKSPACE
@@ -162,7 +162,7 @@ def test_gdn_workspace_bytes_with_sequence_split():
     assert ws(2, 777, 3, 4, nseg=5) == split(8, 13, 5, 777, 3)  # 3 x 4 + 1
     assert ws(2, 777, 3, 4, nseg=1000) == split(8, 13, 13, 777, 1)  # one chunk each
     # fp32 I/O: the chunk workspace also holds the fp16 K / Q rows
-    f32base = 4 * (18 * (58368 + 32768 + 4) + 4 * 4)
+    f32base = 4 * (18 * (58368 + 49152 + 4) + 4 * 4)
     assert ws(1, 1100, 2, 4, f32=True, nseg=4) == (f32base + 255) // 256 * 256 + 4 * 4 * 3 * 65536 + rows(4, 1100, 5)
     # invalid requests
     lib = tsa.load()

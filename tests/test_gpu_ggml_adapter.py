@@ -93,9 +93,14 @@ def test_fp32_views_of_a_fused_projection(dev, T):
     torch.cuda.synchronize()
     assert out.dtype == torch.float32 and torch.equal(out.cpu(), o_ref)
     assert torch.equal(ts_out.cpu(), s_ref)
-    # the fp32 path on fp16-exact inputs carries the fp16 path's state bit for bit (its outputs
-    # may differ from the fp16 path's in the last rounding, tests/test_gpu_gdn.py covers that)
-    assert torch.equal(s_ref, s16)
+    # on fp16-exact inputs the decode and token-serial fp32 paths (T < 32) carry the fp16 path's
+    # state bit for bit (their outputs may differ in the last rounding, tests/test_gpu_gdn.py
+    # covers that); the chunked fp32 path takes its W S state operand and W's A operand as
+    # fp16 hi + lo pairs, so its state agrees with the fp16 path's to the latter's rounding
+    if T < 32:
+        assert torch.equal(s_ref, s16)
+    else:
+        assert float((s_ref - s16).abs().max() / s16.abs().max()) < 3e-4
     assert torch.equal(ts_in.cpu(), torch.from_numpy(st))        # input state untouched
     assert bool((outbuf[:, :, 1] == 7.0).all())                    # the gaps untouched
 

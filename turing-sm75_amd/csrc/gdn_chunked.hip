@@ -59,7 +59,11 @@ constexpr int kWsChunk = kWsG + kC * 16;    // 58368 B, multiple of 256
 // rows in fp16, unswizzled [64 t][128], for the carry's copies (LDS-DMA cannot convert)
 constexpr int kWsK = kWsChunk;
 constexpr int kWsQ = kWsK + kC * kD * 2;
-constexpr int kWsChunkF32 = kWsQ + kC * kD * 2;  // 91136 B
+// and the low halves of the K rows (K - fp16(K), fp16): the state update takes K as an exact
+// hi + lo pair, since rounding the fp32 K to one fp16 operand there is most of the fp32 path's
+// state error (~2.3e-4 of 3.4e-4 on the reference's own inputs, numpy model)
+constexpr int kWsKlo = kWsQ + kC * kD * 2;
+constexpr int kWsChunkF32 = kWsKlo + kC * kD * 2;  // 107520 B
 template <bool kF32> constexpr int ws_chunk() { return kF32 ? kWsChunkF32 : kWsChunk; }
 
 // Ready flags, after all chunk workspaces: one word per (b, h, chunk), then an abort word per
@@ -178,6 +182,23 @@ __device__ __forceinline__ uint4 load8h(const float* p) {
                        (half_t)b.x, (half_t)b.y, (half_t)b.z, (half_t)b.w};
     return __builtin_bit_cast(uint4, h);
 }
+// The same 8 fp32 elements as an exact pair of fp16 halves: hi = fp16(x), lo = fp16(x - hi).
+__device__ __forceinline__ void load8hl(const float* p, uint4& hi, uint4& lo) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    half8_t h, l;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        h[e] = (half_t)x[e];
+        l[e] = (half_t)(x[e] - (float)h[e]);
+    }
+    hi = __builtin_bit_cast(uint4, h);
+    lo = __builtin_bit_cast(uint4, l);
+}
+__device__ __forceinline__ void load8hl(const half_t* p, uint4& hi, uint4& lo) {
+    hi = *reinterpret_cast<const uint4*>(p);
+    lo = make_uint4(0, 0, 0, 0);
+}
 
 // ----------------------------------------------------------------------------------
 // Prep
@@ -228,6 +249,8 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
                const float* __restrict__ beta, GdnRawGates gates, unsigned char* __restrict__ ws,
                unsigned* __restrict__ flags, int T, int Hq, int Hv, int nch, int BHv) {
     __shared__ __align__(16) PrepLds sm;
+    // fp32 I/O: the low fp16 halves of the chunk's V rows (swizzled like V), 16 KiB more LDS
+    __shared__ __align__(16) half_t vlo_lds[std::is_same<TIO, float>::value ? kC * kD : 8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hi = lane >> 5;
     // chunk-major: workgroups are dispatched in the order the carry consumes chunks, and
     // (b, h, chunk) lands on the XCD of the head's carry workgroups when BHv % 8 == 0
@@ -251,13 +274,15 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
         gx = kFused ? gates.a[bt * Hv + h] : g_log[bt * Hv + h];
         gy = kFused ? gates.b[bt * Hv + h] : beta[bt * Hv + h];
     }
-    uint4 kreg[4], vreg[4];
+    // with fp32 I/O K and V also keep their low fp16 halves: K_lo goes to the workspace for the
+    // carry's state update, V_lo feeds the U product as a second B operand
+    uint4 kreg[4], vreg[4], klo[4], vlo[4];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int id = it * kThreads + tid;
         const size_t bt = (size_t)b * T + min(t0 + (id >> 4), lastt);
-        kreg[it] = load8h(k + (bt * Hq + hq) * kD + (id & 15) * 8);
-        vreg[it] = load8h(v + (bt * Hv + h) * kD + (id & 15) * 8);
+        load8hl(k + (bt * Hq + hq) * kD + (id & 15) * 8, kreg[it], klo[it]);
+        load8hl(v + (bt * Hv + h) * kD + (id & 15) * 8, vreg[it], vlo[it]);
     }
     half8_t qa[kD / 16];
     const int qt_row = t0 + 32 * mt + (lane & 31);
@@ -272,7 +297,10 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
         const int r = id >> 4, c = id & 15;
         const uint4 kv = t0 + r > lastt ? make_uint4(0, 0, 0, 0) : kreg[it];
         *reinterpret_cast<uint4*>(sm.K + tile_off(r, c)) = kv;
-        if (kF32) store_dev(wsc + kWsK + (size_t)(r * kD + c * 8) * 2, kv);
+        if (kF32) {
+            store_dev(wsc + kWsK + (size_t)(r * kD + c * 8) * 2, kv);
+            store_dev(wsc + kWsKlo + (size_t)(r * kD + c * 8) * 2, t0 + r > lastt ? make_uint4(0, 0, 0, 0) : klo[it]);
+        }
         if (kFused) {  // the row's 16 threads are 16 consecutive lanes of one wave
             const half8_t k8 = __builtin_bit_cast(half8_t, kv);
             float ss = 0.f;
@@ -463,16 +491,14 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
             for (int qd = 0; qd < 8; ++qd) x[qd] = (16 * ks + 8 * hi + qd <= trow) ? tv[qd] : 0.f;
         };
         {
+            // With fp32 I/O, W's A operand Tm diag(beta e^G) is taken as an exact pair of fp16
+            // halves (two MFMAs per step): with the carry's W S state operand also split, the
+            // state error of a slowly decaying gate halves (numpy model: 4.6e-5 -> 2.2e-5 at
+            // T = 2048).  The fp16-I/O path keeps one operand: the pair cost 3 % of a call at
+            // 32 heads, T = 4096 (A/B on one box).  One output tile at a time, its Tm operands
+            // re-read per tile: two accumulators and a second operand would not fit the 128
+            // registers of four workgroups per CU.
             float16_t w_acc[2];
-            half8_t aw[4];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                if (ks >= nks) break;
-                float x[8];
-                tm_row(ks, x);
-#pragma unroll
-                for (int qd = 0; qd < 8; ++qd) aw[ks][qd] = (half_t)(x[qd] * sm.bg[16 * ks + 8 * hi + qd]);
-            }
 #pragma unroll
             for (int n2 = 0; n2 < 2; ++n2) {
                 const int ntw = 2 * (wave & 1) + n2;
@@ -480,10 +506,20 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
                     if (ks >= nks) break;
+                    float x[8];
+                    tm_row(ks, x);
+                    half8_t awh, awl;
+#pragma unroll
+                    for (int qd = 0; qd < 8; ++qd) {
+                        const float y = x[qd] * sm.bg[16 * ks + 8 * hi + qd];
+                        awh[qd] = (half_t)y;
+                        awl[qd] = (half_t)(y - (float)awh[qd]);
+                    }
                     const int row0 = 16 * ks + 8 * hi;
                     const int col0 = 32 * ntw + 16 * (g16 & 1);
                     const half8_t bk = cat8(tile_read_tr(sm.K, row0, col0), tile_read_tr(sm.K, row0 + 4, col0));
-                    w_acc[n2] = mfma32(aw[ks], bk, w_acc[n2]);
+                    w_acc[n2] = mfma32(awh, bk, w_acc[n2]);
+                    if (kF32) w_acc[n2] = mfma32(awl, bk, w_acc[n2]);
                 }
             }
             lds_barrier();  // every wave's K reads done: W is staged over K
@@ -514,8 +550,10 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
 #pragma unroll
         for (int it = 0; it < 4; ++it) {  // V rows past T (loaded from the last row) are zero
             const int id = it * kThreads + tid;
-            *reinterpret_cast<uint4*>(sm.x.V + tile_off(id >> 4, id & 15)) =
-                t0 + (id >> 4) > lastt ? make_uint4(0, 0, 0, 0) : vreg[it];
+            const bool past = t0 + (id >> 4) > lastt;
+            *reinterpret_cast<uint4*>(sm.x.V + tile_off(id >> 4, id & 15)) = past ? make_uint4(0, 0, 0, 0) : vreg[it];
+            if (kF32)
+                *reinterpret_cast<uint4*>(vlo_lds + tile_off(id >> 4, id & 15)) = past ? make_uint4(0, 0, 0, 0) : vlo[it];
         }
         lds_barrier();
 #pragma unroll
@@ -530,6 +568,10 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
                 const half8_t bv = cat8(tile_read_tr(sm.x.V, row0, col0), tile_read_tr(sm.x.V, row0 + 4, col0));
                 u_acc[n2] = mfma32(au[ks], bv, u_acc[n2]);
                 u_acc[n2] = mfma32(al[ks], bv, u_acc[n2]);
+                if (kF32) {  // the low half of the fp32 V (lo x lo is below fp32 rounding)
+                    const half8_t bvl = cat8(tile_read_tr(vlo_lds, row0, col0), tile_read_tr(vlo_lds, row0 + 4, col0));
+                    u_acc[n2] = mfma32(au[ks], bvl, u_acc[n2]);
+                }
             }
         }
     }
@@ -603,6 +645,15 @@ typedef __attribute__((address_space(3))) void* lds_void_t;
 // and computed once, so an instruction costs a scalar M0 write and the DMA itself.
 constexpr int kDmaN = 66, kDmaChain = 41;
 constexpr int kDmaEOut = 65;  // a 512-byte copy: lanes 0-31 only
+// With fp32 I/O the output waves load their operands from memory into registers and the out
+// slots hold instead the low halves of the chain chunk's K rows (K_lo, 16 KiB): instructions
+// 41 .. 56 copy them, swizzled like K, from the chunk's workspace.
+constexpr int kDmaNF32 = kDmaChain + 16;
+template <bool kF32> constexpr int dma_n() { return kF32 ? kDmaNF32 : kDmaN; }
+__device__ __forceinline__ unsigned dma_src_off_klo(int i, int lane) {
+    const int P = i * 64 + lane, row = P >> 4, cch = (P & 15) ^ swz(row);
+    return kWsKlo + row * kD * 2 + cch * 16;
+}
 
 // Source byte offset of instruction n for this lane, from the instruction's base pointer:
 // the row base of the chunk's first token (K / Q tiles, rows at rowbytes apart, rows
@@ -667,11 +718,15 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
                                          const unsigned* fl, unsigned wait_ticks,
                                          int* err, unsigned rowbytes, size_t chunk_bytes, int pair,
                                          int T, int nch) {
-    constexpr int kJ = (kDmaN - W + 3) / 4;
+    constexpr int kJ = (dma_n<kF32>() - W + 3) / 4;
     const int lane = threadIdx.x & 63;
     unsigned off[kJ];
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) off[j] = dma_src_off(W + 4 * j, lane, rowbytes, pair, kC - 1);
+    for (int j = 0; j < kJ; ++j) {
+        const int n = W + 4 * j;
+        off[j] = kF32 && n >= kDmaChain ? dma_src_off_klo(n - kDmaChain, lane)
+                                        : dma_src_off(n, lane, rowbytes, pair, kC - 1);
+    }
     // slot_lds: cs[0], cs[1], os[0], os[1]
     auto copies = [&](int pc, int po, int cn, int co) {
         const bool do_c = cn < nch, do_o = co >= 0 && co < nch;
@@ -686,6 +741,10 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
                 const int n = W + 4 * j;
                 const bool chainslot = n < kDmaChain;
                 const int i = chainslot ? n : n - kDmaChain;
+                if (kF32 && !chainslot) {  // K_lo rows of the chain chunk, into its parity's out slot
+                    if (do_c) dma_issue(wc, off[j], slot_lds[2 + pc] + 1024u * i, false, true);
+                    continue;
+                }
                 const bool rows = i < 16;
                 if (chainslot ? !do_c : !do_o) continue;
                 unsigned o = off[j];
@@ -770,8 +829,12 @@ __device__ __forceinline__ ChainOffs chain_offs() {
 // before the first MFMA and a scheduling barrier keeps them there: the MFMAs then find
 // their operands arriving in order instead of waiting on each small batch.
 // us: 1, or 0 for a transition map's chain (U = 0).
+// kLo (fp32 I/O): klo is the chunk's K_lo tile, and the update takes K as an exact hi + lo
+// pair (rounding the fp32 K to one fp16 operand there was ~2.3e-4 of relative state error on
+// the reference's own inputs, numpy model); W S takes the state as hi + lo too (see below).
+template <bool kLo>
 __device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs, uint4* xs, int sl,
-                                           const ChainOffs& off, float us) {
+                                           const ChainOffs& off, float us, const half_t* klo) {
     const int lane = threadIdx.x & 63, g = lane >> 4;
     half8_t aW[4][4];
 #pragma unroll
@@ -801,12 +864,26 @@ __device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs
     for (int kk = 0; kk < 4; ++kk)
         Sb[kk] = half8_t{(half_t)S[2 * kk][0], (half_t)S[2 * kk][1], (half_t)S[2 * kk][2], (half_t)S[2 * kk][3],
                          (half_t)S[2 * kk + 1][0], (half_t)S[2 * kk + 1][1], (half_t)S[2 * kk + 1][2], (half_t)S[2 * kk + 1][3]};
-    // W S, the four row-tile chains interleaved
+    // W S, the four row-tile chains interleaved.  With fp32 I/O (kLo) the state operand is an
+    // exact pair of fp16 halves (hi + lo, a second MFMA per step reusing the W operand; with W's
+    // own A operand split in the prep, the state error of a slowly decaying gate halves, numpy
+    // model); the low halves are formed one k-step at a time, next to their MFMAs.  The fp16-I/O
+    // path keeps one operand: the pair put 16 MFMAs on the chunk step's dependency chain
+    // (+16 % per call at 32 heads, T = 4096, A/B on one box).
     float4_t wsv[4] = {float4_t{}, float4_t{}, float4_t{}, float4_t{}};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+    for (int kk = 0; kk < 4; ++kk) {
+        half8_t Sl;
+        if (kLo) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) wsv[mt] = mfma16(aW[mt][kk], Sb[kk], wsv[mt]);
+            for (int e = 0; e < 8; ++e) Sl[e] = (half_t)(S[2 * kk + (e >> 2)][e & 3] - (float)Sb[kk][e]);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            wsv[mt] = mfma16(aW[mt][kk], Sb[kk], wsv[mt]);
+            if (kLo) wsv[mt] = mfma16(aW[mt][kk], Sl, wsv[mt]);
+        }
+    }
     // Vnew = U - W S (lane: column c, tokens 16mt + 4g + r); Vs = Vnew e^{G_C - G_t} as an
     // exact pair of fp16 halves (hi + lo): its rounding to one fp16 operand was ~3e-4 of
     // relative state error at T = 4096; the second MFMA per step reuses the K^T operand
@@ -839,18 +916,32 @@ __device__ __forceinline__ void chain_step(float4_t (&S)[8], const ChainSlot& cs
             S[m] = mfma16(aK[m][ks], Vl[ks], S[m]);
         }
     }
+    // + K_lo^T Vs hi, one row tile's operands read at a time (the registers of the hoisted K^T
+    // reads above are all in use)
+    if (kLo) {
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const half8_t aKl = cat8(lds_read_tr16(klo + off.k[m] + 32 * ks * kD),
+                                         lds_read_tr16(klo + off.k[m] + (32 * ks + 16) * kD));
+                S[m] = mfma16(aKl, Vs[ks], S[m]);
+            }
+        }
+    }
 }
 
-// Output for one chunk, token tiles {2w, 2w+1} of both strips: O = scale (e^G Q S + Aqk Vnew).
-// With TIO = float the values go straight to the fp32 output (o32: this wave's first token
-// row of the chunk and the workgroup's first column; rows past T are skipped) instead of
-// through the fp16 staging tile.
-template <typename TIO>
-__device__ __forceinline__ void out_step(const OutSlot& os, const uint4 (*xs)[6][64], half_t* ostage,
-                                         int w, float scale, float* o32, size_t o32_row, int rows_left) {
-    const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+// A operands of one output wave's chunk: Q (token tiles 2w, 2w+1, in the state operand's
+// k order), Aqk (perm32 columns) and the factors e^{G_t} qn_t of its D rows.
+struct OutOps {
     half8_t aQ[2][4], aA[2][2];
-    float eg[2][4];
+    float4 eg[2];
+};
+// from the chunk's out slot in LDS (fp16 I/O)
+__device__ __forceinline__ OutOps out_ops_lds(const OutSlot& os, int w) {
+    const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    OutOps op;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int t = 16 * (2 * w + j) + c;
@@ -860,13 +951,49 @@ __device__ __forceinline__ void out_step(const OutSlot& os, const uint4 (*xs)[6]
                 os.Q + t * kD + (((4 * kk + (g >> 1)) ^ swz(t)) << 3) + 4 * (g & 1));
             const half4_t up = *reinterpret_cast<const half4_t*>(
                 os.Q + t * kD + (((4 * kk + 2 + (g >> 1)) ^ swz(t)) << 3) + 4 * (g & 1));
-            aQ[j][kk] = cat8(lo, up);
+            op.aQ[j][kk] = cat8(lo, up);
         }
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            aA[j][ks] = *reinterpret_cast<const half8_t*>(os.A + aqk_off(t, 4 * ks + g));
-        const float4 e4 = *reinterpret_cast<const float4*>(os.E + 16 * (2 * w + j) + 4 * g);
-        eg[j][0] = e4.x; eg[j][1] = e4.y; eg[j][2] = e4.z; eg[j][3] = e4.w;
+            op.aA[j][ks] = *reinterpret_cast<const half8_t*>(os.A + aqk_off(t, 4 * ks + g));
+        op.eg[j] = *reinterpret_cast<const float4*>(os.E + 16 * (2 * w + j) + 4 * g);
+    }
+    return op;
+}
+// from the chunk's workspace (fp32 I/O: the prep's fp16 Q rows, unswizzled)
+__device__ __forceinline__ OutOps out_ops_mem(const unsigned char* wsc, int w) {
+    const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const half_t* Q = reinterpret_cast<const half_t*>(wsc + kWsQ);
+    const half_t* A = reinterpret_cast<const half_t*>(wsc + kWsAqk);
+    const float* E = reinterpret_cast<const float*>(wsc + kWsG);
+    OutOps op;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int t = 16 * (2 * w + j) + c;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+            op.aQ[j][kk] = cat8(*reinterpret_cast<const half4_t*>(Q + t * kD + 32 * kk + 4 * g),
+                                *reinterpret_cast<const half4_t*>(Q + t * kD + 32 * kk + 16 + 4 * g));
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            op.aA[j][ks] = *reinterpret_cast<const half8_t*>(A + t * kC + 8 * (4 * ks + g));
+        op.eg[j] = *reinterpret_cast<const float4*>(E + 16 * (2 * w + j) + 4 * g);
+    }
+    return op;
+}
+
+// Output for one chunk, token tiles {2w, 2w+1} of both strips: O = scale (e^G Q S + Aqk Vnew).
+// With TIO = float the values go straight to the fp32 output (o32: this wave's first token
+// row of the chunk and the workgroup's first column; rows past T are skipped) instead of
+// through the fp16 staging tile.
+template <typename TIO>
+__device__ __forceinline__ void out_step(const OutOps& op, const uint4 (*xs)[6][64], half_t* ostage,
+                                         int w, float scale, float* o32, size_t o32_row, int rows_left) {
+    const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    float eg[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        eg[j][0] = op.eg[j].x; eg[j][1] = op.eg[j].y; eg[j][2] = op.eg[j].z; eg[j][3] = op.eg[j].w;
     }
     half8_t Sb[kStrips][4], Vn[kStrips][2];
 #pragma unroll
@@ -885,9 +1012,9 @@ __device__ __forceinline__ void out_step(const OutSlot& os, const uint4 (*xs)[6]
             qs[j][s] = float4_t{};
             av[j][s] = float4_t{};
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) qs[j][s] = mfma16(aQ[j][kk], Sb[s][kk], qs[j][s]);
+            for (int kk = 0; kk < 4; ++kk) qs[j][s] = mfma16(op.aQ[j][kk], Sb[s][kk], qs[j][s]);
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) av[j][s] = mfma16(aA[j][ks], Vn[s][ks], av[j][s]);
+            for (int ks = 0; ks < 2; ++ks) av[j][s] = mfma16(op.aA[j][ks], Vn[s][ks], av[j][s]);
         }
     }
     if (std::is_same<TIO, float>::value) {
@@ -1023,10 +1150,14 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
     if (chain) {
         const ChainOffs off = chain_offs();
         for (int it = 0; it <= nch; it += 2) {
-            if (it < nch) chain_step(S, sm.cs[0], &sm.XS[0][sl][0][0], sl, off, us);
+            if (it < nch)
+                chain_step<kF32>(S, sm.cs[0], &sm.XS[0][sl][0][0], sl, off, us,
+                                 reinterpret_cast<const half_t*>(&sm.os[0]));
             lds_barrier();  // chain waves issue no vector memory operations in the loop
             if (it + 1 > nch) break;
-            if (it + 1 < nch) chain_step(S, sm.cs[1], &sm.XS[1][sl][0][0], sl, off, us);
+            if (it + 1 < nch)
+                chain_step<kF32>(S, sm.cs[1], &sm.XS[1][sl][0][0], sl, off, us,
+                                 reinterpret_cast<const half_t*>(&sm.os[1]));
             lds_barrier();
         }
     } else if (outw) {
@@ -1041,12 +1172,35 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
         float* o32 = obuf ? obuf + (size_t)(32 * w) * kD + pair * 32
                           : reinterpret_cast<float*>(out) + ((size_t)b * T + c0 * kC + 32 * w) * orow +
                                 (size_t)h * kD + pair * 32;
+        // fp32 I/O: the operands come from memory into registers, Q one chunk ahead (ops[ch & 1]
+        // holds chunk ch's), Aqk and e^G at the step (two full operand sets do not fit beside
+        // the chain's registers); otherwise from the chunk's out slot
+        OutOps ops[2];
+        if (kF32) ops[0] = out_ops_mem(wsh, w);
         auto step = [&](int slot, int ch) {
+            if (kF32) {
+                const OutOps nx = out_ops_mem(wsh + (size_t)min(ch + 1, nch - 1) * ws_chunk<kF32>(), w);
+                if (ch + 1 < nch) {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) ops[slot ^ 1].aQ[j][kk] = nx.aQ[j][kk];
+                }
+                const OutOps cu = out_ops_mem(wsh + (size_t)ch * ws_chunk<kF32>(), w);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) ops[slot].aA[j][ks] = cu.aA[j][ks];
+                    ops[slot].eg[j] = cu.eg[j];
+                }
+            } else {
+                ops[slot] = out_ops_lds(sm.os[slot], w);
+            }
             if (f32out)
-                out_step<float>(sm.os[slot], sm.XS[slot], sm.OS[w], w, scale, o32 + (size_t)ch * kC * o32_row,
+                out_step<float>(ops[slot], sm.XS[slot], sm.OS[w], w, scale, o32 + (size_t)ch * kC * o32_row,
                                 o32_row, Tloc - ch * kC - 32 * w);
             else
-                out_step<TIO>(sm.os[slot], sm.XS[slot], sm.OS[w], w, scale, o32, o32_row, 0);
+                out_step<TIO>(ops[slot], sm.XS[slot], sm.OS[w], w, scale, o32, o32_row, 0);
         };
         for (int it = 0; it <= nch; it += 2) {
             if (!f32out && it >= 2) out_flush(sm.OS[w], out16, b, T, Hv, h, (it - 2) * kC, pair, w, Tloc);
