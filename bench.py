@@ -28,7 +28,9 @@ pair of HIP events around its K launches, on the stream they run on, divided by 
 prefill's per-call state reset is timed alone the same way and subtracted).
 After the timed steps, outside the step, the gated grouped-query attention layer of the
 reference's target model (B=1, 24 query / 4 K/V heads, D=256, S=8192, causal, gate after
-softmax) is timed on its own and reported as the part `attn_gqa_gated`; so is the GDN
+softmax) is timed on its own and reported as the part `attn_gqa_gated` (GQA_MIN_WARMUP launches
+back to back, then GQA_TIMED timed ones: it follows the light decode loop, so like attention it
+needs continuous load before its timed launches); so is the GDN
 recurrence with the layer's pre/post ops at the prefill shape (`gdn_layer_ops`): raw q/k
 and gate projections -> fused chunked prefill -> gated RMSNorm, against the unfused
 pipeline (pre-op pass, chunked prefill, gated RMSNorm); and, for context only, one GPU's
@@ -67,6 +69,9 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 # continuous attention launches right before the timed region, whatever --warmup is (~45 ms
 # at config 3; the power controller's start-up transient lasts ~12 ms)
 ATTN_MIN_WARMUP = 80
+# the same for the gated GQA layer, timed after the light decode loop (~40 ms at 0.81 ms a launch)
+GQA_MIN_WARMUP = 50
+GQA_TIMED = 20
 
 # configuration of each part
 ATTN = dict(B=1, H=32, S=8192, D=128, causal=True)
@@ -541,8 +546,12 @@ def main():
     def gqa():
         tsa.attn_gqa_fwd(gq["q"], gq["k"], gq["v"], gq["gate"], gq["o"], causal=True, stream=stream)
 
-    gqa()
-    n_gqa = max(3, min(K, 10))
+    # continuous GQA load before its timed launches: it follows the HBM-bound decode loop, and
+    # one warm-up launch left its 10 timed launches inside the power controller's start-up
+    # transient (0.384-0.395 of peak against 0.409 at steady state on one box)
+    for _ in range(GQA_MIN_WARMUP):
+        gqa()
+    n_gqa = GQA_TIMED
     e4, e5 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e4.record(stream)
     for _ in range(n_gqa):
@@ -718,7 +727,7 @@ def main():
             "workload": "gated GQA attention fwd B=1 Hq=24 Hkv=4 S=8192 D=256 causal fp16, "
                         "N(0,0.5), gate N(0,1); timed outside the step",
             "value": round(gqa_tflops, 2), "unit": "TFLOP/s", "ms": round(gqa_ms, 5),
-            "flop_per_launch": fg,
+            "flop_per_launch": fg, "warmup_launches": GQA_MIN_WARMUP, "timed_launches": GQA_TIMED,
             "roofline": roof("mfma", gqa_tflops, PEAK_MFMA_F16_TFLOPS, "TFLOP/s", "attn_gqa_gated"),
         },
         "gdn_layer_ops": {
