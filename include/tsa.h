@@ -94,8 +94,8 @@ int tsa_attn_gqa_naive(const void* q, const void* k, const void* v, const void* 
  * :271-292, is only first-order accurate).  dk = dv = 128, chunk = 64.  ws must hold
  * tsa_gdn_chunked_workspace_bytes(...) bytes of device memory, the caller's as the
  * reference driver owns the two-pass scratch (src/gdn_sm75.cu:1341-1346); its contents on
- * entry do not matter (the prep writes every ready flag the carry reads; a call whose two
- * kernels run side by side, TSA_GDN_OVERLAP=1, clears them first), and calls that share one
+ * entry do not matter (in order the two kernels use no ready flags; a call whose two kernels
+ * run side by side, TSA_GDN_OVERLAP=1, clears them first), and calls that share one
  * ws must be ordered on one stream.  With few heads and many chunks (B*Hv <= 21, at least 16
  * chunks) the call splits the sequence into segments (segment state maps with their outputs
  * side by side, a combine, a parallel output fix-up) and the workspace grows by 192 KiB per

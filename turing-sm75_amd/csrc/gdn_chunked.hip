@@ -70,10 +70,11 @@ template <bool kF32> constexpr int ws_chunk() { return kF32 ? kWsChunkF32 : kWsC
 // carry workgroup.  A call that runs the prep beside the carry first clears them with a small
 // kernel on the caller's stream (gdn_flags_clear, a kernel rather than a memset so that a
 // captured graph replays it correctly), so whatever the workspace held before, no flag reads
-// as set before the prep sets it in this call.  A call that runs them in order needs no clear:
-// its prep has set every flag before the carry starts, and the carry zeroes the abort words
-// itself.  The prep writes 1 there once the chunk's workspace is in memory; the carry's DMA
-// waves wait for it before copying the chunk.
+// as set before the prep sets it in this call.  A call that runs them in order writes and
+// reads no flags (both kernels get a null flag pointer: the kernel boundary orders the prep's
+// stores before the carry), and the carry zeroes the abort words itself.  Beside the carry
+// the prep writes 1 there once the chunk's workspace is in memory; the carry's DMA waves wait
+// for it before copying the chunk.
 // A wait gives up after a limit on the 100 MHz real-time counter (2 ms; the environment
 // variable TSA_GDN_CARRY_WAIT_US sets it in microseconds, 0 = give up whenever a chunk is
 // not ready at the first look, which is how the tests exercise the path).  When the prep
@@ -596,11 +597,15 @@ gdn_chunk_prep(const TIO* __restrict__ q, const TIO* __restrict__ k,
         store_dev(wsc + kWsW + (size_t)id * 16, *reinterpret_cast<const uint4*>(sm.K + id * 8));
     }
 
-    // ---- 6. publish: every wave's device-scope stores complete, then the chunk's flag ----
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    if (tid == 0)
-        __hip_atomic_store(flags + (size_t)bh * nch + ch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // ---- 6. publish (beside the carry only): every wave's device-scope stores complete, then
+    // the chunk's flag.  In order the kernel boundary orders the stores before the carry, so
+    // the workgroup ends without waiting for them ----
+    if (flags) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (tid == 0)
+            __hip_atomic_store(flags + (size_t)bh * nch + ch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ----------------------------------------------------------------------------------
@@ -765,6 +770,7 @@ __device__ __forceinline__ void dma_role(const unsigned (&slot_lds)[4], const un
     // its round trip overlaps them and a chunk that is ready costs no wait.  After one
     // timed-out wait, no more waits (the workgroup's results are then discarded).
     auto peek = [&](int n) -> unsigned {
+        if (!fl) return 1u;  // in order after the prep: every chunk is ready
         return n < nch ? __hip_atomic_load(fl + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
     };
     // real-time counter (100 MHz), low 32 bits; readfirstlane keeps the wait loop uniform
@@ -1225,7 +1231,7 @@ gdn_chunk_carry(const TIO* __restrict__ q, const TIO* __restrict__ k,
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.cs[1],
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.os[0],
                                       (unsigned)(uintptr_t)(lds_void_t)(void*)&sm.os[1]};
-        const unsigned* fl = flags + (size_t)bh * nch_all + c0;
+        const unsigned* fl = flags ? flags + (size_t)bh * nch_all + c0 : nullptr;
         int* err = &sm.err[wave - 4];
         switch (wave) {
             case 4: dma_role<0, kF32>(slot_lds, kh, qh, wsh, fl, wait_ticks, err, rowbytes, chunk_bytes, pair, Tloc, nch); break;
@@ -1565,15 +1571,16 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
         hipLaunchKernelGGL(gdn_flags_clear, dim3((nflags + 255) / 256), dim3(256), 0, stream, flags, nflags);
         return hipGetLastError();
     };
-    auto prep = [&](hipStream_t st) {
+    // In order (the prep, then the carry, on one stream) no ready flags are written or read.
+    auto prep = [&](hipStream_t st, bool publish) {
         hipLaunchKernelGGL((gdn_chunk_prep<kFused, TIO>), dim3(BHv * nch), dim3(kThreads), 0, st, Q, K,
-                           static_cast<const TIO*>(v), g_log, beta, gates, W, flags, T, Hq, Hv,
-                           nch, BHv);
+                           static_cast<const TIO*>(v), g_log, beta, gates, W, publish ? flags : nullptr, T,
+                           Hq, Hv, nch, BHv);
         return hipGetLastError();
     };
     auto carry = [&](int mode, unsigned ticks, int units = 1, CarryJob job = CarryJob{}) {
         hipLaunchKernelGGL(gdn_chunk_carry<TIO>, dim3(units * carry_wgs), dim3(kCarryThreads), 0, stream, Q, K,
-                           W, flags, aborts, mode, ticks, state, static_cast<TIO*>(out), T, Hq, Hv, nch, BHv,
+                           W, mode == kCarryInOrder ? nullptr : flags, aborts, mode, ticks, state, static_cast<TIO*>(out), T, Hq, Hv, nch, BHv,
                            scale, job);
         return hipGetLastError();
     };
@@ -1589,7 +1596,7 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
         job.seg = reinterpret_cast<float*>(W + seg_offset(BHv, nch, std::is_same<TIO, float>::value));
         job.oz = job.seg + (size_t)BHv * plan.nseg * kSegSlots * kSegSlotFloats;
         job.om = job.oz + (size_t)BHv * job.Tr * kD;
-        hipError_t e = prep(stream);
+        hipError_t e = prep(stream, false);
         if (e == hipSuccess) e = carry(kCarryInOrder, wait_ticks, 2 * plan.nseg - 1, job);
         if (e == hipSuccess) {
             // state columns per combine workgroup: about one workgroup per CU
@@ -1638,7 +1645,7 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
         if (d.ok && 2 * carry_wgs <= d.cus) side = &d;
     }
     if (!side) {  // in order: no flag clear needed
-        const hipError_t e = prep(stream);
+        const hipError_t e = prep(stream, false);
         return e != hipSuccess ? e : carry(kCarryInOrder, wait_ticks);
     }
     hipError_t e = clear();
@@ -1653,7 +1660,7 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
     e = hipEventRecord(side->fork, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(side->s, side->fork, 0);
     if (e == hipSuccess) e = carry(kCarryBeside, wait_ticks);
-    if (e == hipSuccess) e = prep(side->s);
+    if (e == hipSuccess) e = prep(side->s, true);
     if (e == hipSuccess) e = hipEventRecord(side->join, side->s);
     if (e == hipSuccess) e = hipStreamWaitEvent(stream, side->join, 0);
     if (e == hipSuccess) e = carry(kCarryRetry, kRetryWaitTicks);
@@ -1667,9 +1674,9 @@ hipError_t launch_chunked(const void* q, const void* k, const void* v, const flo
 // passes the array's name to a kernel (on the host it is only a stand-in for the symbol):
 // the device address comes from hipGetSymbolAddress, once per device, on the first call on
 // that device, and is kept in g_scratch.  Every call on a GPU shares that GPU's array and
-// leaves its contents behind: the call runs the prep and the carry in order, so the ready
-// flags it reads are set by its own prep, the carry zeroes the abort words, and the rest of
-// the workspace is written before it is read.  Calls that overlap on one GPU race on the
+// leaves its contents behind: the call runs the prep and the carry in order, so it reads no
+// ready flags, the carry zeroes the abort words, and the rest of the workspace is written
+// before it is read.  Calls that overlap on one GPU race on the
 // array.
 constexpr size_t kScratchBytes = 64ull << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
