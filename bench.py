@@ -197,7 +197,7 @@ def layer_inputs(torch, dev, pre):
 
 def host_info():
     """The host the CPU baseline ran on: its CPU model, the logical CPUs it has, and the CPUs
-    this process may run on (the box's share)."""
+    this process may run on (its share of the machine)."""
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:

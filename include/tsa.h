@@ -38,7 +38,7 @@ enum {
     TSA_OK = 0,
     TSA_ERR_NULL = 1,        /* a required pointer is NULL                           */
     TSA_ERR_SHAPE = 2,       /* a size is < 1, too large, or the shapes disagree      */
-    TSA_ERR_UNSUPPORTED = 3, /* a valid shape this build has no kernel for (e.g. D)  */
+    TSA_ERR_UNSUPPORTED = 3, /* a valid shape this library has no kernel for (e.g. D) */
     TSA_ERR_WORKSPACE = 4,   /* workspace NULL or smaller than *_workspace_bytes     */
     TSA_ERR_LAUNCH = 5,      /* the HIP runtime rejected a launch                    */
     TSA_ERR_ARG = 6,         /* a non-shape argument is invalid (scale not finite...) */

@@ -1,7 +1,8 @@
 """numpy wrapper of oracle/liboracle.so -- the CPU restatement of the reference's naive paths.
 
 TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg, always as the checker or the timed CPU baseline, never as the product.
+cpu_baseline leg, always as the reference results are compared with or the timed CPU
+baseline, never as the product.
 The C++ sources cite the reference file:line each function restates (oracle.h).
 """
 from __future__ import annotations

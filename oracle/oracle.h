@@ -4,7 +4,7 @@
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product (the HIP library under
  * turing-sm75_amd/, its C-ABI, or the drivers) links, loads or calls this code.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
- * and only as the checker / the timed CPU baseline.
+ * and only as the reference results are compared with / the timed CPU baseline.
  *
  * Every function cites the reference file:line it restates (paths are relative to
  * the cookys/turing-sm75 tree).  Layouts:

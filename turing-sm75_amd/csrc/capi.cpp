@@ -61,7 +61,7 @@ extern "C" const char* tsa_strerror(int code) {
         case TSA_OK: return "ok";
         case TSA_ERR_NULL: return "a required pointer is NULL";
         case TSA_ERR_SHAPE: return "invalid shape (size < 1, too large, or inconsistent)";
-        case TSA_ERR_UNSUPPORTED: return "shape not supported by this build (attention: D in {64,128,256}; GDN: dk = dv = 128, chunk = 64)";
+        case TSA_ERR_UNSUPPORTED: return "shape not supported by this library (attention: D in {64,128,256}; GDN: dk = dv = 128, chunk = 64)";
         case TSA_ERR_WORKSPACE: return "workspace is NULL or smaller than the required size";
         case TSA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
         case TSA_ERR_ARG: return "invalid argument (causal not 0/1, scale not finite / not > 0, or eps not finite / not > 0)";
