@@ -124,6 +124,21 @@ def test_t4096_hq16_hv32_slow_decay(dev, orc, kind):
 
 
 @pytest.mark.parametrize("kind", ["chunked", "recurrent"])
+def test_more_carry_workgroups_than_cus(dev, orc, kind):
+    """3 sequences x 32 V-heads: the carry launches 384 workgroups of one CU each, more than
+    the 256 CUs, so a second wave of chain workgroups starts as the first ones finish (and
+    the prep has 3 x 32 x 11 workgroups); with an entering state and a slow gate (measured:
+    chunked 9.8e-5 relative state error, token-serial 6.3e-7)."""
+    rng = np.random.default_rng(414)
+    q, k, v, g, beta, st = _inputs(rng, 3, 700, 16, 32, sstd=0.02)
+    g = (-0.01 * (1 + 0.5 * rng.standard_normal(g.shape))).astype(np.float32)
+    o, s = _gpu(dev, kind, q, k, v, g, beta, st)
+    o_ref, s_ref = orc.gdn_serial(q, k, v, g, beta, st)
+    _check(o, s, o_ref, s_ref, *(TOL[kind] if kind == "chunked" else (2e-3, 1e-4)),
+           label=f"{kind} B=3 T=700 Hq=16 Hv=32")
+
+
+@pytest.mark.parametrize("kind", ["chunked", "recurrent"])
 def test_reference_lcg_shape(dev, orc, kind):
     q, k, v, g, b = orc.gdn_lcg_inputs(512, 16, 48)
     h = lambda a: a.astype(np.float16)[None]
